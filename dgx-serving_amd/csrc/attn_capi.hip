@@ -1,0 +1,336 @@
+// extern "C" layer of the MI355X attention library: knobs, per-device scratch and the entry points declared in
+// include/dgx_attn.h. Host code only; every call returns a hipError_t and never aborts or exits.
+#include "attn_device.h"
+#include "attn_internal.h"
+#include "../../include/dgx_attn.h"
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <mutex>
+#include <string>
+
+using namespace dgx;
+
+namespace {
+
+// ---------------------------------------------------------------- knobs
+// Resolution order of the reference registry (runtime/knobs.h:9-13, 297-303): env > DGX_KNOBS_FILE > unset.
+// Recipe lines are NAME=VALUE with '#' comments.
+const char *knob_raw(const char *name) {
+    if (const char *v = getenv(name)) return v;
+    static std::string path;
+    static std::string cache[8][2];
+    static int ncache = -1;
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
+    if (ncache < 0) {
+        ncache = 0;
+        if (const char *p = getenv("DGX_KNOBS_FILE")) {
+            std::ifstream in(p);
+            std::string line;
+            while (in && std::getline(in, line) && ncache < 8) {
+                const size_t h = line.find('#'); if (h != std::string::npos) line.resize(h);
+                const size_t eq = line.find('='); if (eq == std::string::npos) continue;
+                auto trim = [](std::string t) { const size_t a = t.find_first_not_of(" \t\r"), b = t.find_last_not_of(" \t\r");
+                                                return a == std::string::npos ? std::string() : t.substr(a, b - a + 1); };
+                const std::string k = trim(line.substr(0, eq));
+                if (k.rfind("G4_ATTN", 0) == 0 || k.rfind("G4_KV", 0) == 0) { cache[ncache][0] = k; cache[ncache][1] = trim(line.substr(eq + 1)); ncache++; }
+            }
+        }
+    }
+    for (int i = 0; i < ncache; i++) if (cache[i][0] == name) return cache[i][1].c_str();
+    return nullptr;
+}
+
+int g_kv_override = -1;
+
+int parse_kv_dtype() {
+    const char *v = knob_raw("G4_KV_DTYPE");
+    if (!v || !*v) {
+        const char *split = knob_raw("G4_ATTN_SPLIT");
+        return (split && !strcmp(split, "0")) ? DT_FP32 : DT_F16;
+    }
+    if (!strcmp(v, "fp32")) return DT_FP32;
+    if (!strcmp(v, "f16")) return DT_F16;
+    if (!strcmp(v, "bf16")) return DT_BF16;
+    fprintf(stderr, "Invalid G4_KV_DTYPE=%s (fp32, f16 or bf16)\n", v);
+    return -1;
+}
+
+int parse_chunk() {
+    int c = 256;                                  // MI355X default (the GB10 reference defaults to 64)
+    if (const char *v = knob_raw("G4_ATTN_CHUNK")) {
+        c = atoi(v);
+        if (c != 32 && c != 64 && c != 128 && c != 256 && c != 512) {
+            fprintf(stderr, "Invalid G4_ATTN_CHUNK=%s (32, 64, 128, 256 or 512)\n", v);
+            return -1;
+        }
+    }
+    return c;
+}
+
+bool knob_on(const char *name) { const char *v = knob_raw(name); return v && v[0] == '1'; }
+
+// ---------------------------------------------------------------- scratch pools (per device, grow only)
+constexpr int kMaxDev = 64;
+struct Pool {
+    float *m = nullptr, *l = nullptr, *acc = nullptr;
+    size_t cap = 0, acc_cap = 0;
+};
+Pool g_split[kMaxDev], g_flash[kMaxDev];
+std::mutex g_pool_mu;
+
+hipError_t pool_grow(Pool &p, size_t need, size_t hd) {
+    if (hd && need > (SIZE_MAX / sizeof(float)) / hd) return hipErrorInvalidValue;
+    if (p.cap < need) {
+        if (p.m) { hipError_t e = hipFree(p.m); if (e != hipSuccess) return e; p.m = nullptr; }
+        if (p.l) { hipError_t e = hipFree(p.l); if (e != hipSuccess) return e; p.l = nullptr; }
+        p.cap = 0;
+        hipError_t e = hipMalloc(&p.m, need * sizeof(float)); if (e != hipSuccess) return e;
+        e = hipMalloc(&p.l, need * sizeof(float)); if (e != hipSuccess) return e;
+        p.cap = need;
+    }
+    if (p.acc_cap < need * hd) {
+        if (p.acc) { hipError_t e = hipFree(p.acc); if (e != hipSuccess) return e; p.acc = nullptr; }
+        p.acc_cap = 0;
+        hipError_t e = hipMalloc(&p.acc, need * hd * sizeof(float)); if (e != hipSuccess) return e;
+        p.acc_cap = need * hd;
+    }
+    return hipSuccess;
+}
+
+hipError_t pool_for(Pool *pools, Pool *&out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
+    out = &pools[dev];
+    return hipSuccess;
+}
+
+float resolve_scale(float scale, int HD) { return scale > 0.f ? scale : 1.0f / sqrtf((float)HD); }
+
+bool valid_hd(int HD) { return HD == 128 || HD == 256 || HD == 512; }
+bool valid_dtype(int d) { return d == DT_FP32 || d == DT_F16 || d == DT_BF16; }
+
+// Flash-path split size for short query runs (the reference's FD_SPLIT_KV, attention_flash.cuh:11).
+constexpr int kFlashChunk = 512;
+// Key split of the prefill kernel in the drop-in flash entry points: a fixed absolute boundary, so a prompt's
+// result does not depend on how it is chunked.
+constexpr int kPrefillSplit = 512;
+// Query tokens up to which dgx_flash_attn runs the split kernel (decode, verify, trees of <= 32 nodes).
+constexpr int kFlashShortSq = 32;
+
+Problem make_problem(const void *Q, int qt, const void *K, const void *V, int kvt, void *O, int ot, float *lse,
+                     int nseq, int T, int NQ, int NKV, int HD, long kv_stride, int pos_mode, int base, int pos_step,
+                     const int *pos_arr, const unsigned *anc, int max_pos, float scale, int window) {
+    Problem p;
+    p.Q = Q; p.q_dtype = qt; p.K = K; p.V = V; p.kv_dtype = kvt; p.O = O; p.o_dtype = ot; p.lse = lse;
+    p.nseq = nseq; p.T = T; p.NQ = NQ; p.NKV = NKV; p.HD = HD; p.kv_stride = kv_stride;
+    p.pos_mode = pos_mode; p.base = base; p.pos_step = pos_step; p.pos_arr = pos_arr;
+    p.anc = reinterpret_cast<const uint32_t *>(anc); p.max_pos = max_pos;
+    p.scale = resolve_scale(scale, HD); p.window = window < 0 ? 0 : window;
+    return p;
+}
+
+hipError_t run_split(const Problem &p, int chunk, Pool &pool, int ns_cap, hipStream_t st) {
+    Partials part{pool.m, pool.l, pool.acc, ns_cap};
+    hipError_t e = launch_split(p, chunk, part, st);
+    if (e != hipSuccess) return e;
+    return launch_combine(p, chunk, part, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dgx_kv_dtype(void) {
+    if (g_kv_override >= 0) return g_kv_override;
+    static const int dt = parse_kv_dtype();
+    return dt;
+}
+void dgx_kv_force_fp32(const char *why) {
+    if (g_kv_override == DT_FP32) return;
+    const char *v = knob_raw("G4_KV_DTYPE");
+    if (v && strcmp(v, "fp32")) fprintf(stderr, "G4_KV_DTYPE ignored (%s): fp32 KV\n", why ? why : "");
+    g_kv_override = DT_FP32;
+}
+size_t dgx_kv_elem(void) { return dgx_kv_dtype() == DT_FP32 ? 4 : 2; }
+
+int dgx_attn_split_chunk(void) {
+    static const int c = parse_chunk();
+    return c;
+}
+int dgx_attn_split_ns_cap(int max_len) {
+    const int C = dgx_attn_split_chunk();
+    if (C <= 0 || max_len < 0) return -1;
+    return (max_len + C - 1) / C;
+}
+
+hipError_t dgx_attn_split_reserve(int rows, int NQ, int max_len, int hd_max) {
+    if (rows < 0 || NQ <= 0 || max_len < 0 || hd_max <= 0) return hipErrorInvalidValue;
+    const int ns = dgx_attn_split_ns_cap(max_len);
+    if (ns < 0) return hipErrorInvalidValue;
+    Pool *pool; hipError_t e = pool_for(g_split, pool); if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(g_pool_mu);
+    return pool_grow(*pool, (size_t)rows * NQ * ns, (size_t)hd_max);
+}
+
+hipError_t dgx_attn_decode_split(const float *Q, const void *Kc, const void *Vc, int kv_dtype, float *O, float *lse,
+                                 int rows, int NQ, int NKV, int HD, int base, int pos_step, const int *pos_arr,
+                                 int max_pos, long kv_stride, int ns_cap, hipStream_t st, float scale, int window) {
+    if (rows == 0) return hipSuccess;
+    if (!Q || !Kc || !Vc || !O || rows < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || !valid_hd(HD) || max_pos < 0 ||
+        !valid_dtype(kv_dtype))
+        return hipErrorInvalidValue;
+    const int C = dgx_attn_split_chunk();
+    if (C <= 0) return hipErrorInvalidValue;
+    Pool *pool; hipError_t e = pool_for(g_split, pool); if (e != hipSuccess) return e;
+    if (max_pos / C + 1 > ns_cap || (size_t)rows * NQ * ns_cap > pool->cap || (size_t)rows * NQ * ns_cap * HD > pool->acc_cap) {
+        fprintf(stderr, "[attn_split] scratch not reserved: rows=%d NQ=%d ns_cap=%d max_pos=%d\n", rows, NQ, ns_cap, max_pos);
+        return hipErrorInvalidValue;
+    }
+    if (kv_dtype == DT_FP32) {
+        if (lse) return hipErrorInvalidValue;   // the fp32 path keeps the reference's outputs (O only)
+        return launch_scalar_rows(Q, (const float *)Kc, (const float *)Vc, O, rows, NQ, NKV, HD, base, pos_step, pos_arr,
+                                  kv_stride, resolve_scale(scale, HD), window, knob_on("G4_ATTN_DIAG_REVERSE") ? 1 : 0, st);
+    }
+    // Rows that share one KV (kv_stride = 0) form one sequence so every K/V tile is read once for all of them.
+    const bool shared = kv_stride == 0;
+    const Problem p = make_problem(Q, DT_FP32, Kc, Vc, kv_dtype, O, DT_FP32, lse, shared ? 1 : rows, shared ? rows : 1,
+                                   NQ, NKV, HD, kv_stride, 0, base, pos_step, pos_arr, nullptr, max_pos, scale, window);
+    return run_split(p, C, *pool, ns_cap, st);
+}
+
+hipError_t dgx_flash_attn_reserve(int Sq, int NQ, int base, int HD) {
+    if (Sq < 0 || NQ <= 0 || base < 0 || !valid_hd(HD)) return hipErrorInvalidValue;
+    Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
+    const int C = Sq <= kFlashShortSq ? kFlashChunk : kPrefillSplit;
+    const size_t ns = (size_t)(base + Sq) / C + 1;
+    std::lock_guard<std::mutex> lock(g_pool_mu);
+    return pool_grow(*pool, (size_t)Sq * NQ * ns, (size_t)HD);
+}
+
+hipError_t dgx_flash_attn(const float *Q, const void *Kc, const void *Vc, int kv_dtype, float *O, float *lse,
+                          int Sq, int NQ, int NKV, int HD, int base, hipStream_t st, const unsigned *anc,
+                          float scale, int window) {
+    if (Sq == 0) return hipSuccess;
+    if (!Q || !Kc || !Vc || !O || Sq < 0 || base < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || !valid_hd(HD) ||
+        !valid_dtype(kv_dtype))
+        return hipErrorInvalidValue;
+    // The reference's flash path takes a caller scale of exactly 0 as "default" and any other value as given.
+    const float sc = scale == 0.f ? 1.0f / sqrtf((float)HD) : scale;
+    hipError_t e = dgx_flash_attn_reserve(Sq, NQ, base, HD);
+    if (e != hipSuccess) return e;
+    Pool *pool; e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
+    Problem p = make_problem(Q, DT_FP32, Kc, Vc, kv_dtype, O, DT_FP32, lse, 1, Sq, NQ, NKV, HD, 0, 1, base, 1, nullptr,
+                             anc, base + Sq - 1, 1.f, window);
+    p.scale = sc;
+    if (Sq <= kFlashShortSq) {
+        const int ns = (base + Sq - 1) / kFlashChunk + 1;
+        return run_split(p, kFlashChunk, *pool, ns, st);
+    }
+    Partials part{pool->m, pool->l, pool->acc, (base + Sq - 1) / kPrefillSplit + 1};
+    return launch_prefill(p, kPrefillSplit, part, st);
+}
+
+hipError_t dgx_flash_attn_v2(const float *Q, const void *Kc, const void *Vc, int kv_dtype, float *O, float *lse,
+                             int Sq, int NQ, int NKV, int HD, int base, hipStream_t st, float scale, int window,
+                             int f16_mma) {
+    (void)f16_mma;
+    if (Sq == 0) return hipSuccess;
+    if (!Q || !Kc || !Vc || !O || Sq < 0 || base < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || !valid_hd(HD) ||
+        !valid_dtype(kv_dtype))
+        return hipErrorInvalidValue;
+    Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
+    const int ns = (base + Sq - 1) / kPrefillSplit + 1;
+    {
+        std::lock_guard<std::mutex> lock(g_pool_mu);
+        e = pool_grow(*pool, (size_t)Sq * NQ * ns, (size_t)HD);
+        if (e != hipSuccess) return e;
+    }
+    const Problem p = make_problem(Q, DT_FP32, Kc, Vc, kv_dtype, O, DT_FP32, lse, 1, Sq, NQ, NKV, HD, 0, 1, base, 1,
+                                   nullptr, nullptr, base + Sq - 1, scale, window);
+    Partials part{pool->m, pool->l, pool->acc, ns};
+    return launch_prefill(p, kPrefillSplit, part, st);
+}
+
+hipError_t dgx_attn(const float *Q, const float *K, const float *V, float *O, int S, int NQ, int NKV, int HD,
+                    hipStream_t st, float scale, int window) {
+    if (S == 0) return hipSuccess;
+    if (!Q || !K || !V || !O || S < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || HD <= 0 || HD > 512) return hipErrorInvalidValue;
+    return launch_scalar_prefill(Q, K, V, O, S, NQ, NKV, HD, resolve_scale(scale, HD), window < 0 ? 0 : window, st);
+}
+
+hipError_t dgx_attn_decode(const float *Q, const float *Kc, const float *Vc, float *O, int Sq, int NQ, int NKV, int HD,
+                           int base, hipStream_t st, float scale, int window) {
+    if (Sq == 0) return hipSuccess;
+    if (!Q || !Kc || !Vc || !O || Sq < 0 || base < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || HD <= 0 || HD > 512)
+        return hipErrorInvalidValue;
+    return launch_scalar_decode(Q, Kc, Vc, O, 1, Sq, NQ, NKV, HD, base, 0, nullptr, resolve_scale(scale, HD),
+                                window < 0 ? 0 : window, knob_on("G4_ATTN_DIAG_REVERSE") ? 1 : 0, st);
+}
+
+hipError_t dgx_attn_decode_batch(const float *Q, const float *Kc, const float *Vc, float *O, int B, int NQ, int NKV,
+                                 int HD, int base, long kv_stride, hipStream_t st, float scale, int window,
+                                 const int *base_b) {
+    if (B == 0) return hipSuccess;
+    if (!Q || !Kc || !Vc || !O || B < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || HD <= 0 || HD > 512)
+        return hipErrorInvalidValue;
+    return launch_scalar_decode(Q, Kc, Vc, O, B, 1, NQ, NKV, HD, base, kv_stride, base_b, resolve_scale(scale, HD),
+                                window < 0 ? 0 : window, knob_on("G4_ATTN_DIAG_REVERSE") ? 1 : 0, st);
+}
+
+hipError_t dgx_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int which, hipStream_t st) {
+    if (n && (!src || !dst)) return hipErrorInvalidValue;
+    if (!valid_dtype(kv_dtype)) return hipErrorInvalidValue;
+    return launch_kv_store(src, dst, n, kv_dtype, which, knob_on("G4_KV_STATS") ? 1 : 0, st);
+}
+hipError_t dgx_kv_stats(unsigned out[4]) { return read_kv_stats(out); }
+
+hipError_t dgx_attn_batch(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
+                          int o_dtype, float *lse, int B, int Tq, int NQ, int NKV, int HD, const int *base_b, int base,
+                          long kv_stride, const unsigned *anc, int max_pos, int chunk, hipStream_t st, float scale,
+                          int window) {
+    if (B == 0 || Tq == 0) return hipSuccess;
+    if (!Q || !Kc || !Vc || !O || B < 0 || Tq < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || !valid_hd(HD) || max_pos < 0 ||
+        !valid_dtype(q_dtype) || !valid_dtype(o_dtype) || kv_dtype == DT_FP32 || !valid_dtype(kv_dtype))
+        return hipErrorInvalidValue;
+    if (B > 1 && kv_stride == 0 && !base_b) return hipErrorInvalidValue;
+    const int C = chunk > 0 ? chunk : dgx_attn_split_chunk();
+    if (C <= 0 || C % 32) return hipErrorInvalidValue;
+    Pool *pool; hipError_t e = pool_for(g_split, pool); if (e != hipSuccess) return e;
+    const int ns = max_pos / C + 1;
+    if ((size_t)B * Tq * NQ * ns > pool->cap || (size_t)B * Tq * NQ * ns * HD > pool->acc_cap) return hipErrorInvalidValue;
+    const Problem p = make_problem(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, B, Tq, NQ, NKV, HD, kv_stride, 1, base,
+                                   1, base_b, anc, max_pos, scale, window);
+    return run_split(p, C, *pool, ns, st);
+}
+
+hipError_t dgx_attn_prefill(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
+                            int o_dtype, float *lse, int nseq, int Sq, int NQ, int NKV, int HD, const int *base_b,
+                            int base, long kv_stride, int max_pos, int kv_split, hipStream_t st, float scale,
+                            int window) {
+    if (nseq == 0 || Sq == 0) return hipSuccess;
+    if (!Q || !Kc || !Vc || !O || nseq < 0 || Sq < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || !valid_hd(HD) ||
+        max_pos < 0 || !valid_dtype(q_dtype) || !valid_dtype(o_dtype) || !valid_dtype(kv_dtype) || kv_split < 0 ||
+        kv_split % 32)
+        return hipErrorInvalidValue;
+    Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
+    const int ns = kv_split > 0 ? max_pos / kv_split + 1 : 1;
+    if (kv_split > 0) {
+        std::lock_guard<std::mutex> lock(g_pool_mu);
+        e = pool_grow(*pool, (size_t)nseq * Sq * NQ * ns, (size_t)HD);
+        if (e != hipSuccess) return e;
+    }
+    const Problem p = make_problem(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, nseq, Sq, NQ, NKV, HD, kv_stride, 1,
+                                   base, 1, base_b, nullptr, max_pos, scale, window);
+    Partials part{pool->m, pool->l, pool->acc, ns};
+    return launch_prefill(p, kv_split, part, st);
+}
+
+const char *dgx_attn_version(void) { return "dgx-attn-mi355x 0.1 (gfx950)"; }
+
+}  // extern "C"

@@ -1,0 +1,71 @@
+// Internal launch descriptors shared by the kernels and the C-ABI layer (not part of the public interface).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dgx {
+
+// A batch of `nseq` sequences, each with `T` query tokens over its own KV cache (K/V at seq * kv_stride elements).
+// Token (s, t) has global row index r = s * T + t (Q/O/LSE are [r][NQ][HD] / [r][NQ]).
+// Its position is
+//   pos_mode 0: pos_arr ? pos_arr[r] : base + r * pos_step              (launch_attn_decode_split rows)
+//   pos_mode 1: (pos_arr ? pos_arr[s] : base) + t                        (a sequence of consecutive tokens)
+// With anc, the tree of sequence s starts at tb = position of token (s, 0) and anc[r] masks keys >= tb.
+struct Problem {
+    const void *Q; int q_dtype;
+    const void *K; const void *V; int kv_dtype;
+    void *O; int o_dtype;
+    float *lse;                       // optional [rows, NQ], natural log
+    int nseq, T, NQ, NKV, HD;
+    long kv_stride;
+    int pos_mode, base, pos_step;
+    const int *pos_arr;
+    const uint32_t *anc;
+    int max_pos;                      // host-side upper bound of every position (sizes the split grid)
+    float scale;                      // resolved (> 0)
+    int window;
+};
+
+// Split-KV partials in scratch: index (r * NQ + h) * ns_cap + c; m and l in the log2 domain (m = max of
+// scale*log2(e)*q.k, l = sum of 2^(t - m)), acc = sum 2^(t - m) v, unnormalised.
+struct Partials {
+    float *m, *l, *acc;
+    int ns_cap;
+};
+
+// Position of token t of sequence s, and the first key of its sliding window.
+__device__ __forceinline__ int tok_pos(const Problem &p, int s, int t) {
+    if (p.pos_mode == 0) {
+        const int r = s * p.T + t;
+        return p.pos_arr ? p.pos_arr[r] : p.base + r * p.pos_step;
+    }
+    return (p.pos_arr ? p.pos_arr[s] : p.base) + t;
+}
+__device__ __forceinline__ int win_lo(int pos, int window) {
+    return (window > 0 && pos - window + 1 > 0) ? pos - window + 1 : 0;
+}
+
+// Split-KV decode / verify / tree kernel (waves split the keys of a chunk, small query-row tiles).
+hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipStream_t st);
+// Flash prefill kernel (waves split query rows, K/V tiles shared through LDS). kv_split = 0: one pass per row
+// tile writing O directly; kv_split > 0: keys cut at absolute multiples of kv_split, partials + combine.
+hipError_t launch_prefill(const Problem &p, int kv_split, const Partials &part, hipStream_t st);
+// LSE combine of split partials for every (row, head).
+hipError_t launch_combine(const Problem &p, int chunk, const Partials &part, hipStream_t st);
+// Scratch requirement (rows*NQ*ns_cap) of a problem at a given chunk.
+size_t partial_rows(const Problem &p, int chunk);
+
+// fp32 scalar kernels of the reference's attention.cuh (small-shape prefill and smem-free decode).
+hipError_t launch_scalar_prefill(const float *Q, const float *K, const float *V, float *O, int S, int NQ, int NKV,
+                                 int HD, float scale, int window, hipStream_t st);
+hipError_t launch_scalar_decode(const float *Q, const float *Kc, const float *Vc, float *O, int nseq, int Sq,
+                                int NQ, int NKV, int HD, int base, long kv_stride, const int *base_b, float scale,
+                                int window, int reverse, hipStream_t st);
+hipError_t launch_scalar_rows(const float *Q, const float *Kc, const float *Vc, float *O, int rows, int NQ, int NKV,
+                              int HD, int base, int pos_step, const int *pos_arr, long kv_stride, float scale,
+                              int window, int reverse, hipStream_t st);
+hipError_t launch_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int which, int stats,
+                           hipStream_t st);
+hipError_t read_kv_stats(unsigned out[4]);
+
+}  // namespace dgx

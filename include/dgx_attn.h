@@ -1,0 +1,130 @@
+/* dgx_attn.h - C ABI of the MI355X (gfx950) attention library for hyunlord/dgx-serving.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t, returns a hipError_t
+ * (hipSuccess = 0) and never aborts. The C++ header dgx_attn.hpp wraps these under the reference's own
+ * launcher names and turns a failure into the reference's fprintf + abort().
+ *
+ * Layouts (unchanged from the reference, kernels/attention_decode_split.cuh:13-15):
+ *   Q, O      [rows, NQ, HD]              (fp32 at the drop-in entry points)
+ *   K/V cache [len, NKV, HD] per sequence; a batch is [B, max_len, NKV, HD] with
+ *             kv_stride = max_len * NKV * HD elements between sequences
+ *   lse       optional [rows, NQ] fp32, natural-log log-sum-exp of scale * q.k over the attended keys
+ *             (the reference keeps it private; pass NULL to skip)
+ * KV dtype codes are the reference's enum (kernels/kv_store.cuh:20): 0 = fp32, 1 = f16, 2 = bf16.
+ * Q/O dtype codes of the native entry points use the same codes.
+ * scale = 0 selects 1/sqrt(HD); window = 0 is plain causal, window = w keeps keys [pos - w + 1, pos].
+ *
+ * Threading: calls on one device are stream-ordered; library scratch is per device and shared by calls, so
+ * calls that run concurrently on different streams of one device must not share a scratch pool (the decode
+ * split pool and the flash pool are separate, as in the reference).
+ */
+#ifndef DGX_ATTN_H
+#define DGX_ATTN_H
+#include <stddef.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DGX_DT_FP32 0
+#define DGX_DT_F16 1
+#define DGX_DT_BF16 2
+
+/* ---- knobs (runtime/knobs.h registry semantics: env > DGX_KNOBS_FILE recipe > default) ---- */
+
+/* Process-wide KV storage dtype from G4_KV_DTYPE (fp32 | f16 | bf16; unset -> f16, or fp32 when
+ * G4_ATTN_SPLIT=0). Returns -1 for an invalid value (the C++ wrapper exits 1 like the reference).
+ * Replaces g4_kv_dtype(), kernels/kv_store.cuh:23-35. */
+int dgx_kv_dtype(void);
+/* Force fp32 KV for this process (MoE models). Replaces g4_kv_force_fp32(), kernels/kv_store.cuh:37-41. */
+void dgx_kv_force_fp32(const char *why);
+/* Bytes per stored KV element (4 or 2). Replaces g4_kv_elem(), kernels/kv_store.cuh:42. */
+size_t dgx_kv_elem(void);
+
+/* Split-KV chunk from G4_ATTN_CHUNK (32, 64, 128, 256 or 512; unset -> 256 on MI355X). -1 if invalid.
+ * Replaces attn_split_chunk(), kernels/attention_decode_split.cuh:26-37. */
+int dgx_attn_split_chunk(void);
+/* ceil(max_len / chunk). Replaces attn_split_ns_cap(), kernels/attention_decode_split.cuh:173. */
+int dgx_attn_split_ns_cap(int max_len);
+/* Reserve the decode-split scratch (never shrinks) on the current device; call before graph capture.
+ * Replaces attn_split_reserve(), kernels/attention_decode_split.cuh:174-188. */
+hipError_t dgx_attn_split_reserve(int rows, int NQ, int max_len, int hd_max);
+
+/* ---- drop-in launchers ---- */
+
+/* Split-KV decode/verify/batch rows. Row r has position pos_arr ? pos_arr[r] : base + r * pos_step and KV at
+ * Kc + r * kv_stride (kv_stride = 0: rows share one sequence's KV, e.g. verify). max_pos bounds every row
+ * position (host), ns_cap = dgx_attn_split_ns_cap(max_len) of the reservation. Chunk = dgx_attn_split_chunk().
+ * Returns hipErrorInvalidValue when the scratch is not reserved (the reference aborts, :210-213) or the shape
+ * is unsupported. HD in {128, 256, 512}, NQ / NKV <= 64.
+ * Replaces launch_attn_decode_split(), kernels/attention_decode_split.cuh:205-231. */
+hipError_t dgx_attn_decode_split(const float *Q, const void *Kc, const void *Vc, int kv_dtype, float *O, float *lse,
+                                 int rows, int NQ, int NKV, int HD, int base, int pos_step, const int *pos_arr,
+                                 int max_pos, long kv_stride, int ns_cap, hipStream_t st, float scale, int window);
+
+/* Flash attention over a KV cache: Sq query tokens at positions base .. base+Sq-1, causal, optional sliding
+ * window, optional tree mask anc[Sq] (key j >= base attended iff bit j-base of anc[q], j-base < 32).
+ * Its scratch grows inside the call when needed (as the reference's does); pre-size it with
+ * dgx_flash_attn_reserve before graph capture.
+ * Replaces launch_flash_attn<KV>() / launch_flash_attn2bs<HD,BC,NW,KV>(), kernels/attention_flash.cuh:273-306. */
+hipError_t dgx_flash_attn(const float *Q, const void *Kc, const void *Vc, int kv_dtype, float *O, float *lse,
+                          int Sq, int NQ, int NKV, int HD, int base, hipStream_t st, const unsigned *anc,
+                          float scale, int window);
+/* Pre-size the flash scratch for Sq tokens at base. Replaces reserve_flash_attn_scratch(), attention_flash.cuh:236. */
+hipError_t dgx_flash_attn_reserve(int Sq, int NQ, int base, int HD);
+
+/* Prefill / chunked prefill (base > 0 = chunk over a cached prefix). f16_mma: operand precision request of the
+ * reference; here the MFMA operand format always follows the cache (f16 cache: f16, bf16/fp32 cache: bf16).
+ * Replaces launch_flash_attn_v2<KV>(), kernels/attention_flash_v2.cuh:284-292. */
+hipError_t dgx_flash_attn_v2(const float *Q, const void *Kc, const void *Vc, int kv_dtype, float *O, float *lse,
+                             int Sq, int NQ, int NKV, int HD, int base, hipStream_t st, float scale, int window,
+                             int f16_mma);
+
+/* fp32 causal prefill over fp32 K/V [S, NKV, HD] (no S <= HD limit). Replaces launch_attn(), attention.cuh:72-79. */
+hipError_t dgx_attn(const float *Q, const float *K, const float *V, float *O, int S, int NQ, int NKV, int HD,
+                    hipStream_t st, float scale, int window);
+/* fp32 decode/verify over an fp32 cache (no shared-memory context limit). Honors G4_ATTN_DIAG_REVERSE.
+ * Replaces launch_attn_decode(), attention.cuh:137-146. */
+hipError_t dgx_attn_decode(const float *Q, const float *Kc, const float *Vc, float *O, int Sq, int NQ, int NKV, int HD,
+                           int base, hipStream_t st, float scale, int window);
+/* fp32 batch decode: B sequences, one token each at base_b ? base_b[b] : base, KV at b * kv_stride.
+ * Replaces launch_attn_decode_batch(), attention.cuh:189-198. */
+hipError_t dgx_attn_decode_batch(const float *Q, const float *Kc, const float *Vc, float *O, int B, int NQ, int NKV,
+                                 int HD, int base, long kv_stride, hipStream_t st, float scale, int window,
+                                 const int *base_b);
+
+/* fp32 -> cache dtype store (RN-even), which = 0 for K, 1 for V; counts non-finite / max |x| with G4_KV_STATS=1.
+ * dst already offset by the caller (kv_at). Replaces kv_store() / kv_store_kernel, kernels/kv_store.cuh:76-113. */
+hipError_t dgx_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int which, hipStream_t st);
+/* Read the G4_KV_STATS counters {nonfinite K, nonfinite V, max|K| bits, max|V| bits} (kv_store.cuh:86-98). */
+hipError_t dgx_kv_stats(unsigned out[4]);
+
+/* ---- native entry points (16-bit Q/O, one ragged launch, explicit chunking) ---- */
+
+/* One launch over B sequences x Tq query tokens (decode: Tq = 1; tree verify: Tq nodes). Token i of sequence b
+ * is at position (base_b ? base_b[b] : base) + i, its KV at Kc + b * kv_stride; anc[B * Tq] optional tree masks
+ * relative to the sequence's first token. max_pos bounds every position (host). chunk = split size (multiple of
+ * 32; 0 -> dgx_attn_split_chunk()). Uses the decode-split scratch, which must hold B*Tq*NQ*(max_pos/chunk+1)
+ * partials (dgx_attn_split_reserve(B*Tq, NQ, max_pos+1, HD) with the same chunk).
+ * No reference counterpart in one call: it replaces the per-slot loops of launch_flash_attn at
+ * models/qwen35_batch.cu:165-167 (decode) and :333-335 (tree verify). */
+hipError_t dgx_attn_batch(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
+                          int o_dtype, float *lse, int B, int Tq, int NQ, int NKV, int HD, const int *base_b, int base,
+                          long kv_stride, const unsigned *anc, int max_pos, int chunk, hipStream_t st, float scale,
+                          int window);
+/* Prefill with explicit key split (kv_split = 0: none; else a multiple of 32, partials + combine for rows that
+ * span splits) over nseq sequences of Sq tokens at (base_b ? base_b[s] : base) + i. Uses the flash scratch
+ * (grown in the call when needed). Native form of launch_flash_attn_v2 (attention_flash_v2.cuh:284-292). */
+hipError_t dgx_attn_prefill(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
+                            int o_dtype, float *lse, int nseq, int Sq, int NQ, int NKV, int HD, const int *base_b,
+                            int base, long kv_stride, int max_pos, int kv_split, hipStream_t st, float scale,
+                            int window);
+
+/* Library version string. */
+const char *dgx_attn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DGX_ATTN_H */

@@ -1,0 +1,171 @@
+"""TEST INFRASTRUCTURE ONLY: numpy/ctypes front end of the C++ CPU oracle (attn_oracle.cpp).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this module, as the checker or as the
+timed CPU baseline. Nothing in the product (dgx-serving_amd/) imports it.
+
+Every function follows the reference file:line named in attn_oracle.cpp. Pinning (which check fixes each
+function) is listed in tests/test_oracle.py.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P, I, F, U16, U32, U64, S = (ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_uint16, ctypes.c_uint32,
+                                     ctypes.c_uint64, ctypes.c_size_t)
+        L.oracle_f32_to_f16.argtypes = [F]; L.oracle_f32_to_f16.restype = U16
+        L.oracle_f16_to_f32.argtypes = [U16]; L.oracle_f16_to_f32.restype = F
+        L.oracle_f32_to_bf16.argtypes = [F]; L.oracle_f32_to_bf16.restype = U16
+        L.oracle_bf16_to_f32.argtypes = [U16]; L.oracle_bf16_to_f32.restype = F
+        for n in ("oracle_round_f16", "oracle_round_bf16"):
+            getattr(L, n).argtypes = [P, P, P, S]; getattr(L, n).restype = None
+        for n in ("oracle_gen_lcg", "oracle_gen_lcg24", "oracle_gen_lcg16"):
+            getattr(L, n).argtypes = [P, P, S]; getattr(L, n).restype = None
+        L.oracle_gen_xorshift.argtypes = [P, P, S]; L.oracle_gen_xorshift.restype = None
+        L.oracle_gen_normal.argtypes = [U64, U64, F, F, P, S]; L.oracle_gen_normal.restype = None
+        L.oracle_gen_uniform_int.argtypes = [U64, I, I, P, I]; L.oracle_gen_uniform_int.restype = None
+        L.oracle_tree_anc.argtypes = [P, I, P]; L.oracle_tree_anc.restype = I
+        L.oracle_tree_kw.argtypes = [I, I, P, P]; L.oracle_tree_kw.restype = I
+        L.oracle_tree_random.argtypes = [U64, I, I, I, P, P]; L.oracle_tree_random.restype = I
+        L.oracle_attention.argtypes = [P, P, P, P, P, P, P, I, I, I, I, F, I, I, P, P, I]
+        L.oracle_attention.restype = I
+        L.oracle_attention_split.argtypes = [P, P, P, P, P, I, I, I, I, F, I, I, P, P]
+        L.oracle_attention_split.restype = I
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ------------------------------------------------------------------ rounding
+def round_f16(x):
+    """RN-even fp32 -> f16 (values as fp32, bits as uint16)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    vals = np.empty_like(x); bits = np.empty(x.shape, np.uint16)
+    lib().oracle_round_f16(_p(x), _p(vals), _p(bits), x.size)
+    return vals, bits
+
+
+def round_bf16(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    vals = np.empty_like(x); bits = np.empty(x.shape, np.uint16)
+    lib().oracle_round_bf16(_p(x), _p(vals), _p(bits), x.size)
+    return vals, bits
+
+
+def round_to(x, dtype):
+    """Round to a storage dtype code (0 fp32, 1 f16, 2 bf16): returns (fp32 values, raw storage array)."""
+    if dtype == 0:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        return x, x
+    return round_f16(x) if dtype == 1 else round_bf16(x)
+
+
+# ------------------------------------------------------------------ generators
+def gen_lcg(seed, n):
+    st = (ctypes.c_uint32 * 1)(seed); out = np.empty(n, np.float32)
+    lib().oracle_gen_lcg(ctypes.cast(st, ctypes.c_void_p), _p(out), n)
+    return out, st[0]
+
+
+def gen_lcg24(seed, n):
+    st = (ctypes.c_uint32 * 1)(seed); out = np.empty(n, np.float32)
+    lib().oracle_gen_lcg24(ctypes.cast(st, ctypes.c_void_p), _p(out), n)
+    return out, st[0]
+
+
+def gen_lcg16(seed, n):
+    st = (ctypes.c_uint32 * 1)(seed); out = np.empty(n, np.float32)
+    lib().oracle_gen_lcg16(ctypes.cast(st, ctypes.c_void_p), _p(out), n)
+    return out, st[0]
+
+
+def gen_xorshift(seed, n):
+    st = (ctypes.c_uint64 * 1)(seed); out = np.empty(n, np.float32)
+    lib().oracle_gen_xorshift(ctypes.cast(st, ctypes.c_void_p), _p(out), n)
+    return out, st[0]
+
+
+def gen_normal(seed, n, mean=0.0, sd=1.0, offset=0):
+    out = np.empty(n, np.float32)
+    lib().oracle_gen_normal(seed, offset, mean, sd, _p(out), n)
+    return out
+
+
+def gen_uniform_int(seed, lo, hi, n):
+    out = np.empty(n, np.int32)
+    lib().oracle_gen_uniform_int(seed, lo, hi, _p(out), n)
+    return out
+
+
+# ------------------------------------------------------------------ trees
+def tree_anc(parent):
+    parent = np.ascontiguousarray(parent, dtype=np.int32)
+    anc = np.empty(len(parent), np.uint32)
+    rc = lib().oracle_tree_anc(_p(parent), len(parent), _p(anc))
+    if rc:
+        raise ValueError(f"bad tree ({rc})")
+    return anc
+
+
+def tree_kw(K, W):
+    parent = np.empty(K + W, np.int32); depth = np.empty(K + W, np.int32)
+    if lib().oracle_tree_kw(K, W, _p(parent), _p(depth)) < 0:
+        raise ValueError("bad K/W")
+    return parent, depth
+
+
+def tree_random(seed, n, width=2, max_depth=7):
+    parent = np.empty(n, np.int32); depth = np.empty(n, np.int32)
+    if lib().oracle_tree_random(seed, n, width, max_depth, _p(parent), _p(depth)) < 0:
+        raise ValueError("cannot build tree")
+    return parent, depth
+
+
+# ------------------------------------------------------------------ attention
+def attention(q, k, v, kv_off, pos, NQ, NKV, HD, scale=0.0, window=0, anc=None, tree_base=None, mode=0, nthreads=0):
+    """fp64 (mode 0) or fp32-host (mode 1) attention; returns (out [T,NQ,HD] f64, lse [T,NQ] f64)."""
+    q = np.ascontiguousarray(q, np.float32); k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    kv_off = np.ascontiguousarray(kv_off, np.int64); pos = np.ascontiguousarray(pos, np.int32)
+    T = len(pos)
+    assert q.size == T * NQ * HD
+    if anc is not None:
+        anc = np.ascontiguousarray(anc, np.uint32); tree_base = np.ascontiguousarray(tree_base, np.int32)
+    out = np.empty((T, NQ, HD), np.float64); lse = np.empty((T, NQ), np.float64)
+    rc = lib().oracle_attention(_p(q), _p(k), _p(v), _p(kv_off), _p(pos), _p(anc), _p(tree_base), T, NQ, NKV, HD,
+                                float(scale), int(window), int(mode), _p(out), _p(lse), int(nthreads))
+    if rc:
+        raise ValueError("oracle_attention: bad arguments")
+    return out, lse
+
+
+def attention_split(q, k, v, kv_off, pos, NQ, NKV, HD, C, scale=0.0, window=0):
+    q = np.ascontiguousarray(q, np.float32); k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    kv_off = np.ascontiguousarray(kv_off, np.int64); pos = np.ascontiguousarray(pos, np.int32)
+    T = len(pos)
+    out = np.empty((T, NQ, HD), np.float64); lse = np.empty((T, NQ), np.float64)
+    rc = lib().oracle_attention_split(_p(q), _p(k), _p(v), _p(kv_off), _p(pos), T, NQ, NKV, HD, float(scale),
+                                      int(window), int(C), _p(out), _p(lse))
+    if rc:
+        raise ValueError("oracle_attention_split: bad arguments")
+    return out, lse

@@ -1,0 +1,82 @@
+"""GPU parity of speculative tree-verify attention (ancestor bitmask) against the oracle.
+
+Re-expresses tests/test_treeattn.cu (chain mask == causal bit for bit; a tree node equals the linear path of
+its ancestors) and BASELINE.json config 5 (B=16 sequences x 8 tree nodes, committed context U[2048,16384],
+Qwen3.5 full-attention shape, f16 KV) in one ragged launch.
+"""
+import numpy as np
+import pytest
+import torch
+
+import dgx_attn as A
+import oracle
+from helpers import assert_close, dev, dev_bits, normal_cache, oracle_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def test_chain_equals_causal_and_branch_equals_linear():
+    HD, NQ, NKV, base, Sq = 128, 4, 4, 2, 4
+    vals, _ = oracle.gen_lcg16(77, Sq * NQ * HD + 2 * (base + Sq) * NKV * HD)
+    q = vals[:Sq * NQ * HD]
+    kraw = vals[Sq * NQ * HD:Sq * NQ * HD + (base + Sq) * NKV * HD]
+    vraw = vals[Sq * NQ * HD + (base + Sq) * NKV * HD:]
+    k, kb = oracle.round_bf16(kraw)
+    v, vb = oracle.round_bf16(vraw)
+    Q, Kd, Vd = dev(q), dev_bits(kb, 2), dev_bits(vb, 2)
+    On = torch.empty(Sq * NQ * HD, device="cuda"); Oa = torch.empty_like(On)
+    A.flash_attn(Q, Kd, Vd, On, Sq, NQ, NKV, HD, base)
+    A.flash_attn(Q, Kd, Vd, Oa, Sq, NQ, NKV, HD, base, anc=dev(np.array([1, 3, 7, 15], np.int32)))
+    torch.cuda.synchronize()
+    assert torch.equal(On.view(torch.int32), Oa.view(torch.int32)), "chain mask differs from causal"
+    # branch: parent = [-1, 0, 0, 1]; node 2 (second child of the root) sees prefix + root + itself
+    anc = oracle.tree_anc(np.array([-1, 0, 0, 1]))
+    assert list(anc) == [1, 3, 5, 11]
+    Ot = torch.empty_like(On)
+    A.flash_attn(Q, Kd, Vd, Ot, Sq, NQ, NKV, HD, base, anc=dev(anc.view(np.int32)))
+    # linear reference: [prefix, R, C1], queries R and C1, causal
+    row = NKV * HD
+    k2 = np.concatenate([kb[:base * row], kb[base * row:(base + 1) * row], kb[(base + 2) * row:(base + 3) * row]])
+    v2 = np.concatenate([vb[:base * row], vb[base * row:(base + 1) * row], vb[(base + 2) * row:(base + 3) * row]])
+    q2 = np.concatenate([q[:NQ * HD], q[2 * NQ * HD:3 * NQ * HD]])
+    O2 = torch.empty(2 * NQ * HD, device="cuda")
+    A.flash_attn(dev(q2), dev_bits(k2, 2), dev_bits(v2, 2), O2, 2, NQ, NKV, HD, base)
+    torch.cuda.synchronize()
+    e = (Ot[2 * NQ * HD:3 * NQ * HD] - O2[NQ * HD:]).abs().max().item()
+    assert e < 1e-6, f"tree node vs linear path: {e:.3e}"
+    # and the whole tree against the oracle
+    ref, _ = oracle_rows(q, k, v, np.zeros(Sq, np.int64), base + np.arange(Sq), NQ, NKV, HD, anc=anc,
+                         tree_base=np.full(Sq, base))
+    assert_close(Ot.cpu().numpy().reshape(Sq, NQ, HD), ref, "tree vs oracle")
+
+
+@pytest.mark.parametrize("tree", ["random8", "kw9"])
+def test_config5_batched_tree_verify(tree):
+    """B=16, tree nodes per sequence (seeded 2-wide depth<=7 tree of 8 nodes, or the
+    reference's K7W2 shape of 9 nodes), committed L ~ U[2048, 16384], Hq=24, Hkv=4, hd=256, f16 KV."""
+    B, NQ, NKV, HD = 16, 24, 4, 256
+    committed = oracle.gen_uniform_int(55, 2048, 16384, B)
+    if tree == "random8":
+        parents = [oracle.tree_random(1000 + b, 8, 2, 7)[0] for b in range(B)]
+    else:
+        parents = [oracle.tree_kw(7, 2)[0] for _ in range(B)]
+    Tq = len(parents[0])
+    anc = np.stack([oracle.tree_anc(p) for p in parents]).astype(np.uint32)
+    ML = 16384 + Tq
+    lens = committed + Tq
+    kv, kd = normal_cache(61, B, ML, NKV, HD, lens, 0.5, 1)
+    vv, vd = normal_cache(62, B, ML, NKV, HD, lens, 0.5, 1)
+    q = oracle.gen_normal(63, B * Tq * NQ * HD)
+    base_b = committed.astype(np.int32)
+    max_pos = int((base_b + Tq - 1).max())
+    A.split_reserve(B * Tq, NQ, max_pos + 1, HD)
+    O = torch.empty(B * Tq * NQ * HD, device="cuda"); lse = torch.empty(B * Tq * NQ, device="cuda")
+    A.attn_batch(dev(q), kd, vd, O, B, Tq, NQ, NKV, HD, dev(base_b), ML * NKV * HD, max_pos, chunk=512,
+                 anc=dev(anc.reshape(-1).view(np.int32)), lse=lse)
+    torch.cuda.synchronize()
+    pos = (base_b[:, None] + np.arange(Tq)[None, :]).reshape(-1)
+    kv_off = np.repeat(np.arange(B, dtype=np.int64) * ML * NKV * HD, Tq)
+    ref, ref_lse = oracle_rows(q, kv, vv, kv_off, pos, NQ, NKV, HD, anc=anc.reshape(-1),
+                               tree_base=np.repeat(base_b, Tq))
+    assert_close(O.cpu().numpy().reshape(B * Tq, NQ, HD), ref, f"config5 {tree}", lse.cpu().numpy().reshape(-1, NQ),
+                 ref_lse)
