@@ -1,0 +1,234 @@
+"""Benchmark of the MI355X attention hot path (BASELINE.json metric).
+
+Headline (`value`): batched split-KV decode at BASELINE config 2 - B=16, Hq=24, Hkv=4, hd=256, f16 KV cache
+[16, 8192, 4, 256], ragged context lengths L_b ~ U[256, 8192] (seeded), split 512 + LSE combine, one query token
+per sequence - as algorithmic HBM GB/s: bytes = sum_b L_b * Hkv * hd * 2 (K and V) * 2 B + |Q| + |O|.
+Alongside: causal flash prefill at config 3 (T=1024, Hq=16, Hkv=8, hd=256, bf16) as TFLOP/s with
+flops = 4 * hd * Hq * sum of attended keys, and the other BASELINE configs in µs per layer call.
+A step is one layer call (one launch of the kernel for decode: the LSE combine is fused).
+
+Timing: W untimed warm-up steps, then exactly K steps between torch.cuda.synchronize() calls, measured with
+HIP events recorded on the stream the kernels are launched on (torch's current stream).
+cpu_baseline: the oracle's fp32 host attention (restating tests/test_kernels.cu:94-108) on the same decode
+inputs, timed on the host cores of this box.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "dgx-serving_amd"))
+import dgx_attn as A  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def timed(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps        # ms per step
+
+
+def decode_workload(seed=2026):
+    B, NQ, NKV, HD, ML = 16, 24, 4, 256, 8192
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(256, ML, size=B, endpoint=True).astype(np.int32)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    K = (torch.randn(B, ML, NKV, HD, device="cuda", generator=g) * 0.5).half()
+    V = (torch.randn(B, ML, NKV, HD, device="cuda", generator=g) * 0.5).half()
+    Q = torch.randn(B * NQ * HD, device="cuda", generator=g).half()
+    O = torch.empty_like(Q)
+    pos = torch.from_numpy(lens - 1).cuda()
+    return dict(B=B, NQ=NQ, NKV=NKV, HD=HD, ML=ML, lens=lens, K=K, V=V, Q=Q, O=O, pos=pos)
+
+
+def run_decode(w, steps, warmup, chunk=512):
+    B, NQ, NKV, HD, ML = w["B"], w["NQ"], w["NKV"], w["HD"], w["ML"]
+    max_pos = int(w["lens"].max()) - 1
+    A.split_reserve(B, NQ, ML, HD)
+    fn = lambda: A.attn_batch(w["Q"], w["K"], w["V"], w["O"], B, 1, NQ, NKV, HD, w["pos"], ML * NKV * HD, max_pos,
+                              chunk=chunk)
+    ms = timed(fn, steps, warmup)
+    nbytes = int(w["lens"].sum()) * NKV * HD * 2 * 2 + 2 * B * NQ * HD * 2
+    return ms, nbytes
+
+
+def run_prefill(steps, warmup, T=1024, NQ=16, NKV=8, HD=256, base=0, window=0, kv_split=0, seed=3):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    L = base + T
+    K = torch.randn(L, NKV, HD, device="cuda", generator=g).bfloat16()
+    V = torch.randn(L, NKV, HD, device="cuda", generator=g).bfloat16()
+    Q = torch.randn(T * NQ * HD, device="cuda", generator=g).bfloat16()
+    O = torch.empty_like(Q)
+    fn = lambda: A.attn_prefill(Q, K, V, O, 1, T, NQ, NKV, HD, base=base, kv_split=kv_split, window=window)
+    ms = timed(fn, steps, warmup)
+    pos = base + np.arange(T, dtype=np.int64)
+    lo = np.maximum(0, pos - window + 1) if window > 0 else np.zeros_like(pos)
+    pairs = int((pos - lo + 1).sum())
+    flops = 4.0 * HD * NQ * pairs
+    return ms, flops
+
+
+def run_tree(steps, warmup, seed=5):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    B, NQ, NKV, HD, Tq = 16, 24, 4, 256, 8
+    rng = np.random.default_rng(seed)
+    committed = rng.integers(2048, 16384, size=B, endpoint=True).astype(np.int32)
+    # 2-wide random tree of 8 nodes in BFS order, depth <= 7 (parents precede children)
+    anc = np.zeros((B, Tq), np.uint32)
+    for b in range(B):
+        par = [-1]; kids = [0] * Tq
+        for j in range(1, Tq):
+            cand = [p for p in range(j) if kids[p] < 2]
+            p = int(rng.choice(cand)); par.append(p); kids[p] += 1
+        for j in range(Tq):
+            m, x = 0, j
+            while x >= 0:
+                m |= 1 << x; x = par[x]
+            anc[b, j] = m
+    ML = 16384 + Tq
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    K = (torch.randn(B, ML, NKV, HD, device="cuda", generator=g) * 0.5).half()
+    V = (torch.randn(B, ML, NKV, HD, device="cuda", generator=g) * 0.5).half()
+    Q = torch.randn(B * Tq * NQ * HD, device="cuda", generator=g).half()
+    O = torch.empty_like(Q)
+    base_b = torch.from_numpy(committed).cuda()
+    ancd = torch.from_numpy(anc.reshape(-1).view(np.int32)).cuda()
+    max_pos = int(committed.max()) + Tq - 1
+    A.split_reserve(B * Tq, NQ, max_pos + 1, HD)
+    fn = lambda: A.attn_batch(Q, K, V, O, B, Tq, NQ, NKV, HD, base_b, ML * NKV * HD, max_pos, chunk=512, anc=ancd)
+    ms = timed(fn, steps, warmup)
+    nbytes = int((committed + Tq).sum()) * NKV * HD * 4 + 2 * Q.numel() * 2
+    return ms, nbytes
+
+
+def run_sliding_decode(steps, warmup, seed=9):
+    B, NQ, NKV, HD, W = 8, 16, 8, 256, 1024
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(1024, 32768, size=B, endpoint=True).astype(np.int32)
+    ML = 32768
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    K = torch.randn(B, ML, NKV, HD, device="cuda", generator=g).bfloat16()
+    V = torch.randn(B, ML, NKV, HD, device="cuda", generator=g).bfloat16()
+    Q = torch.randn(B * NQ * HD, device="cuda", generator=g).bfloat16()
+    O = torch.empty_like(Q)
+    pos = torch.from_numpy(lens - 1).cuda()
+    A.split_reserve(B, NQ, ML, HD)
+    fn = lambda: A.attn_batch(Q, K, V, O, B, 1, NQ, NKV, HD, pos, ML * NKV * HD, int(lens.max()) - 1, chunk=256,
+                              window=W)
+    ms = timed(fn, steps, warmup)
+    nbytes = B * W * NKV * HD * 4 + 2 * Q.numel() * 2
+    return ms, nbytes
+
+
+def cpu_baseline(w):
+    """Oracle fp32 host attention over the full decode workload, all host threads, on the GPU's inputs."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    B, NQ, NKV, HD, ML = w["B"], w["NQ"], w["NKV"], w["HD"], w["ML"]
+    lens = w["lens"]
+    Lmax = int(lens.max())
+    K = w["K"][:, :Lmax].float().cpu().numpy()
+    V = w["V"][:, :Lmax].float().cpu().numpy()
+    q = w["Q"].float().cpu().numpy()
+    kv_off = np.arange(B, dtype=np.int64) * Lmax * NKV * HD
+    threads = min(os.cpu_count() or 1, 16)
+    t0 = time.perf_counter()
+    oracle.attention(q, K, V, kv_off, lens - 1, NQ, NKV, HD, mode=1, nthreads=threads)
+    dt = time.perf_counter() - t0
+    nbytes = int(lens.sum()) * NKV * HD * 4 + 2 * B * NQ * HD * 2
+    return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                sample=f"full decode workload (16 rows x 24 heads, sum L = {int(lens.sum())} keys), fp32 host "
+                       f"attention (fp64 dot, fp32 softmax) over {threads} threads, {dt * 1e3:.1f} ms per call")
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the decode kernel from the committed rocprofv3 PMC summary, if present."""
+    path = os.path.join(ROOT, "profiles", "decode_split_b16_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch="):
+            return int(float(line.split("=", 1)[1]))
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["decode", "prefill", "all"], default="all")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (requested --gpus {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    A.lib()
+    out = {}
+    w = decode_workload()
+    ms, nbytes = run_decode(w, args.steps, args.warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    extra = {}
+    if args.only in ("prefill", "all"):
+        pms, pflops = run_prefill(args.steps, args.warmup, kv_split=int(os.environ.get("BENCH_PREFILL_SPLIT", "256")))
+        ptf = pflops / (pms * 1e-3) / 1e12
+        extra["prefill_causal_T1024"] = dict(us=round(pms * 1e3, 2), tflops=round(ptf, 2),
+                                             frac_bf16_peak=round(ptf / BF16_PEAK_TFLOPS, 4))
+    if args.only == "all":
+        cms, cfl = run_prefill(args.steps, args.warmup, T=512, base=4096, kv_split=1024)
+        extra["prefill_chunked_512_over_4096"] = dict(us=round(cms * 1e3, 2), tflops=round(cfl / (cms * 1e-3) / 1e12, 2))
+        sms, sfl = run_prefill(max(args.steps // 4, 10), args.warmup, T=4096, window=1024, kv_split=0)
+        extra["prefill_sliding_T4096_w1024"] = dict(us=round(sms * 1e3, 2), tflops=round(sfl / (sms * 1e-3) / 1e12, 2))
+        dms, dby = run_sliding_decode(args.steps, args.warmup)
+        extra["decode_sliding_B8_w1024"] = dict(us=round(dms * 1e3, 2), gbs=round(dby / (dms * 1e-3) / 1e9, 1))
+        tms, tby = run_tree(args.steps, args.warmup)
+        extra["tree_verify_B16x8"] = dict(us=round(tms * 1e3, 2), gbs=round(tby / (tms * 1e-3) / 1e9, 1))
+    out = {
+        "metric": "decode-attn HBM GB/s (B16 ragged <=8K) + prefill-attn TFLOP/s (T=1024)",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "split-KV GQA decode, B=16 ragged L~U[256,8192], Hq=24 Hkv=4 hd=256 (Qwen3.5-27B "
+                               "full-attention layer), f16 KV [16,8192,4,256], split 512 + fused LSE combine, f16 Q/O",
+                   "global_batch": 16, "seq_len": int(w["lens"].max()), "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+                     "algorithmic_bytes_per_launch": nbytes, "us_per_launch": round(ms * 1e3, 2)},
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(w),
+    }
+    if extra.get("prefill_causal_T1024"):
+        pre = extra["prefill_causal_T1024"]
+        out["prefill"] = {"bound": "mfma", "achieved": pre["tflops"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                          "frac": pre["frac_bf16_peak"], "us_per_launch": pre["us"],
+                          "workload": "causal flash prefill T=1024, Hq=16 Hkv=8 hd=256, bf16 Q/K/V/O"}
+    out["extra"] = extra
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -91,16 +91,49 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4 &a, const u32x4 &b, const f
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// Reductions across the four 16-lane groups that hold one query row (lanes l, l^16, l^32, l^48).
+// 16x16x16 MFMA: A lane l holds A[l % 16][4 * (l / 16) + e], B lane l holds B[4 * (l / 16) + e][l % 16], e = 0..3;
+// D as for 16x16x32.
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma16k16(const u32x2 &a, const u32x2 &b, const f32x4 &c) {
+    if constexpr (F16)
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+}
+
+// LDS transpose read (gfx950 ds_read_b64_tr_b16). Within each 16-lane group g, lane i passes the address of
+// row 4g + i/4, columns 4*(i%4)..+3 of a row-major 16-bit tile; lane n of the group receives column n of
+// rows 4g..4g+3. With rows = keys and columns = head dims this is the A fragment of O^T += V^T P^T for a
+// 16x16x16 MFMA, straight from a row-major V tile.
+typedef short lds_s4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t *p) {
+    const lds_s4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) lds_s4 *)(reinterpret_cast<uintptr_t>(p)));
+    return __builtin_bit_cast(u32x2, r);
+}
+
+// Online-softmax rescale threshold (log2 units): the running reference max of a row moves only when a new score
+// exceeds it by more than this, so unnormalised probabilities stay <= 2^8 and the accumulator is rescaled on a
+// handful of tiles instead of every tile.
+constexpr float kRescaleThreshold = 8.0f;
+
+// Reductions across the four 16-lane groups that hold one query row (lanes l, l^16, l^32, l^48), on the VALU:
+// gfx950's v_permlane16_swap / v_permlane32_swap hand every lane the (even row, odd row) and (low half,
+// high half) pair of a value, so each step is one op and all four lanes combine the operands in the same order
+// (bit-identical results).
 __device__ __forceinline__ float max_over_groups(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float sum_over_groups(float v) {
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 // Reductions across the two 32-lane halves (32x32 MFMA layout: a row lives in lanes l and l^32).
 __device__ __forceinline__ float max_over_halves(float v) { return fmaxf(v, __shfl_xor(v, 32)); }

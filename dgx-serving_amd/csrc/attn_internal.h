@@ -46,7 +46,10 @@ __device__ __forceinline__ int win_lo(int pos, int window) {
 }
 
 // Split-KV decode / verify / tree kernel (waves split the keys of a chunk, small query-row tiles).
-hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipStream_t st);
+// counters: zero-initialised ints, one per (sequence, token tile, kv head) (split_counter_count); when given,
+// the kernel also performs the LSE combine (the last workgroup of each group merges) and leaves them zero.
+hipError_t launch_split(const Problem &p, int chunk, const Partials &part, int *counters, hipStream_t st);
+size_t split_counter_count(const Problem &p);
 // Flash prefill kernel (waves split query rows, K/V tiles shared through LDS). kv_split = 0: one pass per row
 // tile writing O directly; kv_split > 0: keys cut at absolute multiples of kv_split, partials + combine.
 hipError_t launch_prefill(const Problem &p, int kv_split, const Partials &part, hipStream_t st);

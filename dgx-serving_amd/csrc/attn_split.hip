@@ -35,24 +35,76 @@ struct SplitArgs {
     int tpb;        // query tokens per workgroup
     int nchunks;    // token tiles per sequence
     float sl2;      // scale * log2(e)
+    int *counters;  // per (sequence, token tile, kv head) arrival counters for the fused combine, or null
 };
 
-template <int HD, int RB, int NW>
+// LSE combine of one (row, head) for 4 consecutive output dims d4*4..+3, over the row's valid chunks
+// [lo/C, pos/C] in ascending order (attention_decode_split.cuh:147-165): O = sum w_c acc_c / sum w_c l_c with
+// w_c = 2^(m_c - max m). Shared by the fused epilogue and the stand-alone combine kernel, so both produce the
+// same bits.
+// Agent-scope relaxed atomic accesses of the partials: they are written through to the device coherence point
+// and read from it, so workgroups on different XCDs exchange partials without an L2 write-back or invalidate.
+__device__ __forceinline__ void st_agent(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_part(const float *p, bool agent) { return agent ? ld_agent(p) : *p; }
+
+template <int HD>
+__device__ __forceinline__ void combine_row4(const Problem &p, const Partials &part, int C, int s, int t, int h, int d4,
+                                             bool agent = false) {
+    const int r = s * p.T + t;
+    const int pos = tok_pos(p, s, t), lo = win_lo(pos, p.window);
+    const int c_lo = lo / C, c_hi = pos / C;
+    const size_t base = ((size_t)r * p.NQ + h) * part.ns_cap;
+    float mg = kNegInf;
+    for (int c = c_lo; c <= c_hi; c++) mg = fmaxf(mg, ld_part(part.m + base + c, agent));
+    float L = 0.f;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (mg != kNegInf)
+        for (int c = c_lo; c <= c_hi; c++) {
+            const float mc = ld_part(part.m + base + c, agent);
+            if (mc != kNegInf) {
+                const float w = fast_exp2(mc - mg);
+                L += ld_part(part.l + base + c, agent) * w;
+                const float *pa = part.acc + (base + c) * HD + 4 * d4;
+                f32x4 v;
+                if (agent) v = f32x4{ld_agent(pa), ld_agent(pa + 1), ld_agent(pa + 2), ld_agent(pa + 3)};
+                else v = *reinterpret_cast<const f32x4 *>(pa);
+                acc += v * w;
+            }
+        }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const f32x4 o = acc * inv;
+    const size_t oi = ((size_t)r * p.NQ + h) * HD + 4 * d4;
+    if (p.o_dtype == DT_FP32) *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.O) + oi) = o;
+    else {
+        const bool f16 = p.o_dtype == DT_F16;
+        const u32x2 w = u32x2{(uint32_t)f32_to_op(o.x, f16) | ((uint32_t)f32_to_op(o.y, f16) << 16),
+                              (uint32_t)f32_to_op(o.z, f16) | ((uint32_t)f32_to_op(o.w, f16) << 16)};
+        *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(p.O) + oi) = w;
+    }
+    if (p.lse && d4 == 0) p.lse[(size_t)r * p.NQ + h] = (L > 0.f) ? (mg + log2f(L)) * kLn2 : kNegInf;
+}
+
+template <int HD, int RB>
 struct SplitCfg {
-    static constexpr int KS = HD / 32;        // QK k-steps
-    static constexpr int DB = HD / 16;        // PV output dim blocks
-    static constexpr int VSTR = HD + 8;       // V tile LDS row stride (16-bit elements)
-    static constexpr int VCH = HD / 16;       // 16-byte V chunks per lane per 32-key tile
-    static constexpr int RR = RB * 16;        // rows per workgroup
-    static constexpr int BSTR = HD + 4;       // merge buffer row stride (floats)
-    static constexpr size_t LDS_TILES = (size_t)NW * 32 * VSTR * 2;
-    static constexpr size_t LDS_MERGE = ((size_t)2 * NW * RR + (size_t)RR * BSTR) * 4;
-    static constexpr size_t LDS = LDS_TILES > LDS_MERGE ? LDS_TILES : LDS_MERGE;
+    static constexpr int NW = 4;              // waves per workgroup; wave w owns head dims [w*HD/4, (w+1)*HD/4)
+    static constexpr int KT = 16;             // keys per tile
+    static constexpr int KS = HD / 32;        // QK k-steps (16x16x32)
+    static constexpr int DBW = HD / 64;       // PV output dim blocks (16x16x16) per wave
+    static constexpr int STR = HD + 8;        // LDS row stride of Q, K and V tiles (16-bit elements)
+    static constexpr int RR = RB * 16;        // query rows per workgroup
+    static constexpr int CPT = KT * HD / 8 / (NW * 64);   // 16-byte chunks per thread per tile (K and V each)
+    static constexpr size_t TILE = (size_t)KT * STR;      // elements of one K or V tile
+    static constexpr size_t LDS = ((size_t)RR * STR + 4 * TILE) * 2;   // Q + (K, V) x double buffer
+    static_assert(CPT >= 1 && (KT * HD / 8) % (NW * 64) == 0, "tile chunks");
 };
 
-template <int HD, int RB, int KVT, int QT, int NW>
-__global__ void __launch_bounds__(NW * 64) split_kernel(const SplitArgs a) {
-    using Cf = SplitCfg<HD, RB, NW>;
+template <int HD, int RB, int KVT, int QT>
+__global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
+    using Cf = SplitCfg<HD, RB>;
+    constexpr int NW = Cf::NW;
     constexpr bool F16 = OpIsF16<KVT>::value;
     using KE = typename Elem<KVT>::T;
     using QE = typename Elem<QT>::T;
@@ -74,233 +126,246 @@ __global__ void __launch_bounds__(NW * 64) split_kernel(const SplitArgs a) {
     const int j_lo = max(c * C, lo_b), j_hi = min(c * C + C, hi_b);
     if (j_lo >= j_hi) return;                                  // chunk outside every row's key range
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, ln = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, ln = lane & 15;
     const size_t krow = (size_t)p.NKV * HD;
     const KE *Kb = reinterpret_cast<const KE *>(p.K) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
     const KE *Vb = reinterpret_cast<const KE *>(p.V) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
+    uint16_t *qs = reinterpret_cast<uint16_t *>(smem);
+    uint16_t *tiles = qs + (size_t)Cf::RR * Cf::STR;           // [buf][K | V][KT][STR]
 
+    // Q rows of the workgroup -> LDS in the MFMA operand format (row rho = token-major (token, head)).
+    for (int i = tid; i < Cf::RR * (HD / 8); i += NW * 64) {
+        const int rho = i / (HD / 8), col = (i % (HD / 8)) * 8;
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (rho < nrows) {
+            const int t = tok0 + rho / GRP, h = kvh * GRP + rho % GRP;
+            v = load8_op<QT, F16>(reinterpret_cast<const QE *>(p.Q) + ((size_t)(seq * p.T + t) * p.NQ + h) * HD + col);
+        }
+        *reinterpret_cast<u32x4 *>(qs + rho * Cf::STR + col) = v;
+    }
     RowMask rm[RB];
-    u32x4 qop[RB][Cf::KS];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
         const int rho = rb * 16 + ln;
         const bool valid = rho < nrows;
-        const int t = tok0 + (valid ? rho / GRP : 0), h = kvh * GRP + (valid ? rho % GRP : 0);
+        const int t = tok0 + (valid ? rho / GRP : 0);
         const int ps = tok_pos(p, seq, t);
         rm[rb].pos = ps; rm[rb].lo = win_lo(ps, p.window); rm[rb].valid = valid;
         rm[rb].tree = p.anc != nullptr;
         rm[rb].anc = p.anc ? p.anc[seq * p.T + t] : 0u;
         rm[rb].tb = p.anc ? tok_pos(p, seq, 0) : 0;
-        const QE *qrow = reinterpret_cast<const QE *>(p.Q) + ((size_t)(seq * p.T + t) * p.NQ + h) * HD + 8 * g;
-#pragma unroll
-        for (int ks = 0; ks < Cf::KS; ks++)
-            qop[rb][ks] = valid ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
     }
 
-    float m[RB], l[RB];
-    f32x4 acc[RB][Cf::DB];
+    // Block-uniform bounds for the unmasked fast path: a tile is "full" when every valid row attends all its keys.
+    int lo_max = 0, pos_min = INT_MAX;
+    for (int t = tok0; t < tok1; t++) {
+        const int ps = tok_pos(p, seq, t);
+        lo_max = max(lo_max, win_lo(ps, p.window));
+        pos_min = min(pos_min, ps);
+    }
+    if (p.anc) pos_min = min(pos_min, tok_pos(p, seq, 0) - 1);   // tree keys are never in the fast path
+
+    // Cooperative tile fetch (global -> registers): chunk q = tid + 256*u -> key q / (HD/8), column (q % (HD/8))*8.
+    // Two register stages keep the loads of tile it+2 in flight while tile it is computed from LDS.
+    u32x4 kr0[Cf::CPT], vr0[Cf::CPT], kr1[Cf::CPT], vr1[Cf::CPT];
+    auto fetch = [&](u32x4 (&kr)[Cf::CPT], u32x4 (&vr)[Cf::CPT], int jt) {
+#pragma unroll
+        for (int u = 0; u < Cf::CPT; u++) {
+            const int q = tid + NW * 64 * u, key = q / (HD / 8), col = (q % (HD / 8)) * 8;
+            const size_t off = (size_t)min(jt + key, hi_b - 1) * krow + col;
+            kr[u] = load8_op<KVT, F16>(Kb + off);
+            vr[u] = load8_op<KVT, F16>(Vb + off);
+        }
+    };
+    auto stash = [&](const u32x4 (&kr)[Cf::CPT], const u32x4 (&vr)[Cf::CPT], int buf) {
+        uint16_t *kt = tiles + (size_t)buf * 2 * Cf::TILE, *vt = kt + Cf::TILE;
+#pragma unroll
+        for (int u = 0; u < Cf::CPT; u++) {
+            const int q = tid + NW * 64 * u, key = q / (HD / 8), col = (q % (HD / 8)) * 8;
+            *reinterpret_cast<u32x4 *>(kt + key * Cf::STR + col) = kr[u];
+            *reinterpret_cast<u32x4 *>(vt + key * Cf::STR + col) = vr[u];
+        }
+    };
+
+    float m[RB], l[RB], mnew[RB];
+    f32x4 acc[RB][Cf::DBW];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
         m[rb] = kNegInf; l[rb] = 0.f;
 #pragma unroll
-        for (int db = 0; db < Cf::DB; db++) acc[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int db = 0; db < Cf::DBW; db++) acc[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    uint16_t *vs = reinterpret_cast<uint16_t *>(smem) + (size_t)wave * 32 * Cf::VSTR;
-    const int ntiles = C / 32;
-    for (int it = wave; it < ntiles; it += NW) {
-        const int jt = c * C + 32 * it;
-        if (jt + 32 <= j_lo || jt >= j_hi) continue;
-        // K fragments: lane (key ln of block kb, group g) holds dims 32*ks + 8*g .. +8.
-        u32x4 kop[2][Cf::KS];
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-            const int key = min(jt + 16 * kb + ln, hi_b - 1);
-            const KE *kp = Kb + (size_t)key * krow + 8 * g;
-#pragma unroll
-            for (int ks = 0; ks < Cf::KS; ks++) kop[kb][ks] = load8_op<KVT, F16>(kp + 32 * ks);
-        }
-        // V tile rows, coalesced: HD/8 lanes per key row.
-        u32x4 vr[Cf::VCH];
-#pragma unroll
-        for (int u = 0; u < Cf::VCH; u++) {
-            const int q = lane + 64 * u, key = q / (HD / 8), col = (q % (HD / 8)) * 8;
-            const int kc = min(jt + key, hi_b - 1);
-            vr[u] = load8_op<KVT, F16>(Vb + (size_t)kc * krow + col);
-        }
-        f32x4 s[RB][2];
+    const int jb = (j_lo / Cf::KT) * Cf::KT;
+    const int ntile = (j_hi - jb + Cf::KT - 1) / Cf::KT;
+    fetch(kr0, vr0, jb);
+    if (ntile > 1) fetch(kr1, vr1, jb + Cf::KT);
+    stash(kr0, vr0, 0);
+    __syncthreads();                                           // Q rows and tile 0 are in LDS
+    constexpr bool QREG = RB * Cf::KS <= 8;                    // Q fragments in registers when they fit
+    u32x4 qreg[QREG ? RB : 1][QREG ? Cf::KS : 1];
+    if constexpr (QREG) {
 #pragma unroll
         for (int rb = 0; rb < RB; rb++)
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
-                f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < Cf::KS; ks++) x = mfma16<F16>(kop[kb][ks], qop[rb][ks], x);
-                s[rb][kb] = x;
-            }
-#pragma unroll
-        for (int u = 0; u < Cf::VCH; u++) {
-            const int q = lane + 64 * u, key = q / (HD / 8), col = (q % (HD / 8)) * 8;
-            *reinterpret_cast<u32x4 *>(vs + key * Cf::VSTR + col) = vr[u];
-        }
-        // Online softmax (log2 domain). Lane holds keys jt + 16*kb + 4*g + i of row ln.
-        u32x4 pop[RB];
-#pragma unroll
-        for (int rb = 0; rb < RB; rb++) {
-            float tv[8], mx = kNegInf;
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int key = jt + 16 * kb + 4 * g + i;
-                    const float v = rm[rb].attends(key) ? s[rb][kb][i] * a.sl2 : kNegInf;
-                    tv[kb * 4 + i] = v; mx = fmaxf(mx, v);
-                }
-            mx = max_over_groups(mx);
-            const float mnew = fmaxf(m[rb], mx);
-            const float alpha = (mnew == kNegInf) ? 1.f : fast_exp2(m[rb] - mnew);
-            float pv[8], ps = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; e++) { pv[e] = (tv[e] == kNegInf) ? 0.f : fast_exp2(tv[e] - mnew); ps += pv[e]; }
-            ps = sum_over_groups(ps);
-            l[rb] = l[rb] * alpha + ps; m[rb] = mnew;
-#pragma unroll
-            for (int db = 0; db < Cf::DB; db++) acc[rb][db] *= alpha;
-            pop[rb] = u32x4{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3]), pack2<F16>(pv[4], pv[5]), pack2<F16>(pv[6], pv[7])};
-        }
-        __builtin_amdgcn_wave_barrier();
-        // O^T += V^T P^T. A fragment: lane (dim 16*db + ln, group g) holds V[key(g, e)][dim] with
-        // key(g, e) = 4g + e (e < 4) or 16 + 4g + e - 4 (e >= 4): the same key order as the P^T registers.
-#pragma unroll
-        for (int db = 0; db < Cf::DB; db++) {
-            const uint16_t *vc = vs + 16 * db + ln;
-            uint16_t x[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int key = (e < 4) ? 4 * g + e : 16 + 4 * g + (e - 4);
-                x[e] = vc[key * Cf::VSTR];
-            }
-            const u32x4 vop = u32x4{(uint32_t)x[0] | ((uint32_t)x[1] << 16), (uint32_t)x[2] | ((uint32_t)x[3] << 16),
-                                    (uint32_t)x[4] | ((uint32_t)x[5] << 16), (uint32_t)x[6] | ((uint32_t)x[7] << 16)};
-#pragma unroll
-            for (int rb = 0; rb < RB; rb++) acc[rb][db] = mfma16<F16>(vop, pop[rb], acc[rb][db]);
-        }
-        __builtin_amdgcn_wave_barrier();
+            for (int ks = 0; ks < Cf::KS; ks++)
+                qreg[rb][ks] = *reinterpret_cast<const u32x4 *>(qs + (rb * 16 + ln) * Cf::STR + 32 * ks + 8 * g);
     }
 
-    // Merge the NW wave states in wave order, then write the chunk partial.
-    __syncthreads();
-    float *redm = reinterpret_cast<float *>(smem), *redl = redm + NW * Cf::RR, *buf = redl + NW * Cf::RR;
-    if (g == 0) {
+    auto compute = [&](int it) {
+        const int jt = jb + Cf::KT * it;
+        const uint16_t *kt = tiles + (size_t)(it & 1) * 2 * Cf::TILE, *vt = kt + Cf::TILE;
+        // S^T[key][row] = K Q^T (every wave computes the whole tile) as two independent MFMA chains.
+        f32x4 s[RB], s2[RB];
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++) { redm[wave * Cf::RR + rb * 16 + ln] = m[rb]; redl[wave * Cf::RR + rb * 16 + ln] = l[rb]; }
+        for (int rb = 0; rb < RB; rb++) s[rb] = s2[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < Cf::KS; ks++) {
+            const u32x4 kf = *reinterpret_cast<const u32x4 *>(kt + ln * Cf::STR + 32 * ks + 8 * g);
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) {
+                u32x4 qf;
+                if constexpr (QREG) qf = qreg[rb][ks];
+                else qf = *reinterpret_cast<const u32x4 *>(qs + (rb * 16 + ln) * Cf::STR + 32 * ks + 8 * g);
+                if (ks & 1) s2[rb] = mfma16<F16>(kf, qf, s2[rb]);
+                else s[rb] = mfma16<F16>(kf, qf, s[rb]);
+            }
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) s[rb] += s2[rb];
+        // Online softmax (log2 domain) with a lazily moved reference max m (see kRescaleThreshold). l holds
+        // this lane's share of the row sum; the four lanes of a row are added once, after the loop.
+        const bool full = jt >= j_lo && jt + Cf::KT <= j_hi && jt >= lo_max && jt + Cf::KT - 1 <= pos_min;
+        u32x2 pop[RB];
+        float tv[RB][4];
+        bool need = false;
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            float mx = kNegInf;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int key = jt + 4 * g + i;
+                const float v = (full || (key >= j_lo && key < j_hi && rm[rb].attends(key))) ? s[rb][i] * a.sl2 : kNegInf;
+                tv[rb][i] = v; mx = fmaxf(mx, v);
+            }
+            mx = max_over_groups(mx);
+            if (mx > m[rb] + kRescaleThreshold) { mnew[rb] = mx; need = true; } else mnew[rb] = m[rb];
+        }
+        if (__any(need)) {
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) {
+                const float alpha = (mnew[rb] == m[rb]) ? 1.f : fast_exp2(m[rb] - mnew[rb]);
+                l[rb] *= alpha; m[rb] = mnew[rb];
+#pragma unroll
+                for (int db = 0; db < Cf::DBW; db++) acc[rb][db] *= alpha;
+            }
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            float pv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) { pv[i] = (tv[rb][i] == kNegInf) ? 0.f : fast_exp2(tv[rb][i] - m[rb]); l[rb] += pv[i]; }
+            pop[rb] = u32x2{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3])};
+        }
+        // O^T[this wave's dims] += V^T P^T (16x16x16): the A fragment is a transposed LDS read of the V tile.
+        const uint16_t *vtr = vt + (4 * g + (ln >> 2)) * Cf::STR + wave * (HD / NW) + 4 * (ln & 3);
+#pragma unroll
+        for (int db = 0; db < Cf::DBW; db++) {
+            const u32x2 vop = lds_read_tr16(vtr + 16 * db);
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) acc[rb][db] = mfma16k16<F16>(vop, pop[rb], acc[rb][db]);
+        }
+    };
+    // Iteration it: fetch tile it+2 into the register stage that held tile it, compute tile it from LDS, stash
+    // tile it+1 (fetched one iteration earlier) into the other LDS buffer, barrier.
+    for (int it = 0; it < ntile; it += 2) {
+        if (it + 2 < ntile) fetch(kr0, vr0, jb + Cf::KT * (it + 2));
+        compute(it);
+        if (it + 1 < ntile) stash(kr1, vr1, 1);
+        __syncthreads();
+        if (it + 1 >= ntile) break;
+        if (it + 3 < ntile) fetch(kr1, vr1, jb + Cf::KT * (it + 3));
+        compute(it + 1);
+        if (it + 2 < ntile) stash(kr0, vr0, 0);
+        __syncthreads();
     }
-    __syncthreads();
-    float f[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) l[rb] = sum_over_groups(l[rb]);
+
+    // Chunk partial: wave w writes its dims of every row; wave 0 writes (m, l). Lane (row ln, group g) holds
+    // O^T[dims w*HD/4 + 16*db + 4g + i][row].
+    const int NQ = p.NQ, ns = a.part.ns_cap;
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
         const int row = rb * 16 + ln;
-        float M = kNegInf;
-        for (int w = 0; w < NW; w++) M = fmaxf(M, redm[w * Cf::RR + row]);
-        f[rb] = (m[rb] == kNegInf) ? 0.f : fast_exp2(m[rb] - M);
-    }
-    for (int w = 0; w < NW; w++) {
-        if (wave == w) {
+        if (row >= nrows) continue;
+        const int r = seq * p.T + tok0 + row / GRP, h = kvh * GRP + row % GRP;
+        const size_t pi = ((size_t)r * NQ + h) * ns + c;
 #pragma unroll
-            for (int rb = 0; rb < RB; rb++) {
-                const int row = rb * 16 + ln;
-                if (row < nrows) {
-#pragma unroll
-                    for (int db = 0; db < Cf::DB; db++) {
-                        f32x4 *dst = reinterpret_cast<f32x4 *>(buf + row * Cf::BSTR + 16 * db + 4 * g);
-                        f32x4 v = acc[rb][db] * f[rb];
-                        if (w > 0) v += *dst;
-                        *dst = v;
-                    }
-                }
-            }
+        for (int db = 0; db < Cf::DBW; db++) {
+            float *dst = a.part.acc + pi * HD + wave * (HD / NW) + 16 * db + 4 * g;
+            const f32x4 v = acc[rb][db];
+            if (a.counters) { st_agent(dst, v.x); st_agent(dst + 1, v.y); st_agent(dst + 2, v.z); st_agent(dst + 3, v.w); }
+            else *reinterpret_cast<f32x4 *>(dst) = v;
         }
-        __syncthreads();
+        if (wave == 0 && g == 0) {
+            if (a.counters) { st_agent(a.part.m + pi, m[rb]); st_agent(a.part.l + pi, l[rb]); }
+            else { a.part.m[pi] = m[rb]; a.part.l[pi] = l[rb]; }
+        }
     }
-    const int NQ = p.NQ, ns = a.part.ns_cap;
-    for (int idx = threadIdx.x; idx < nrows * (HD / 4); idx += NW * 64) {
-        const int row = idx / (HD / 4), d4 = idx % (HD / 4);
-        const int r = seq * p.T + tok0 + row / GRP, h = kvh * GRP + row % GRP;
-        const size_t pi = ((size_t)r * NQ + h) * ns + c;
-        *reinterpret_cast<f32x4 *>(a.part.acc + pi * HD + 4 * d4) = *reinterpret_cast<const f32x4 *>(buf + row * Cf::BSTR + 4 * d4);
+    if (!a.counters) return;
+
+    // Fused combine: the last workgroup of this (sequence, token tile, kv head) to finish merges all chunk
+    // partials of its rows. Partials travel as agent-scope atomics (written through, read from the coherence
+    // point); each wave waits for its stores to complete before the barrier, so the counter increment that
+    // follows is ordered after every partial of the workgroup without any cache-wide write-back.
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int *cnt = a.counters + ((size_t)seq * a.nchunks + tchunk) * p.NKV + kvh;
+    if (threadIdx.x == 0) {
+        // Chunks that exist in the grid and intersect the group's key range (a max_pos below the true positions
+        // drops keys, as in the reference, but keeps the counters consistent).
+        const int expected = min((hi_b - 1) / C, (int)gridDim.x - 1) - lo_b / C + 1;
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (old == expected - 1);
+        if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    for (int row = threadIdx.x; row < nrows; row += NW * 64) {
-        float M = kNegInf;
-        for (int w = 0; w < NW; w++) M = fmaxf(M, redm[w * Cf::RR + row]);
-        float L = 0.f;
-        if (M != kNegInf)
-            for (int w = 0; w < NW; w++) {
-                const float mw = redm[w * Cf::RR + row];
-                if (mw != kNegInf) L += redl[w * Cf::RR + row] * fast_exp2(mw - M);
-            }
-        const int r = seq * p.T + tok0 + row / GRP, h = kvh * GRP + row % GRP;
-        const size_t pi = ((size_t)r * NQ + h) * ns + c;
-        a.part.m[pi] = M; a.part.l[pi] = L;
-    }
+    __syncthreads();
+    if (!s_last) return;
+    for (int idx = threadIdx.x; idx < nrows * (HD / 4); idx += NW * 64)
+        combine_row4<HD>(p, a.part, C, seq, tok0 + (idx / (HD / 4)) / GRP, kvh * GRP + (idx / (HD / 4)) % GRP, idx % (HD / 4),
+                         true);
 }
 
-// LSE combine over the row's valid chunks [lo/C, pos/C] in ascending order
-// (attention_decode_split.cuh:147-165): O = sum w_c acc_c / sum w_c l_c, w_c = 2^(m_c - max m).
-template <int OT>
+// Stand-alone LSE combine (one workgroup per (row, head)); used when no arrival counters are supplied.
+template <int HD>
 __global__ void __launch_bounds__(256) combine_kernel(const Problem p, const Partials part, int C) {
     const int r = blockIdx.x, h = blockIdx.y;
-    const int s = r / p.T, t = r % p.T;
-    const int pos = tok_pos(p, s, t), lo = win_lo(pos, p.window);
-    const int c_lo = lo / C, c_hi = pos / C;
-    const size_t base = ((size_t)r * p.NQ + h) * part.ns_cap;
-    float mg = kNegInf;
-    for (int c = c_lo; c <= c_hi; c++) mg = fmaxf(mg, part.m[base + c]);
-    float L = 0.f;
-    if (mg != kNegInf)
-        for (int c = c_lo; c <= c_hi; c++) {
-            const float mc = part.m[base + c];
-            if (mc != kNegInf) L += part.l[base + c] * fast_exp2(mc - mg);
-        }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    const int HD = p.HD;
-    for (int d = threadIdx.x; d < HD; d += blockDim.x) {
-        float acc = 0.f;
-        if (mg != kNegInf)
-            for (int c = c_lo; c <= c_hi; c++) {
-                const float mc = part.m[base + c];
-                if (mc != kNegInf) acc += part.acc[(base + c) * HD + d] * fast_exp2(mc - mg);
-            }
-        const float o = acc * inv;
-        const size_t oi = ((size_t)r * p.NQ + h) * HD + d;
-        if constexpr (OT == DT_FP32) reinterpret_cast<float *>(p.O)[oi] = o;
-        else reinterpret_cast<uint16_t *>(p.O)[oi] = f32_to_op(o, OT == DT_F16);
-    }
-    if (p.lse && threadIdx.x == 0)
-        p.lse[(size_t)r * p.NQ + h] = (L > 0.f) ? (mg + log2f(L)) * kLn2 : kNegInf;
+    for (int d4 = threadIdx.x; d4 < HD / 4; d4 += blockDim.x) combine_row4<HD>(p, part, C, r / p.T, r % p.T, h, d4);
 }
 
 // ---------------------------------------------------------------- host side
-template <int HD, int RB, int KVT, int QT, int NW>
+template <int HD, int RB, int KVT, int QT>
 static hipError_t launch_split_t(const SplitArgs &a, dim3 grid, hipStream_t st) {
-    using Cf = SplitCfg<HD, RB, NW>;
+    using Cf = SplitCfg<HD, RB>;
     static bool configured = false;
     if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&split_kernel<HD, RB, KVT, QT, NW>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&split_kernel<HD, RB, KVT, QT>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cf::LDS);
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL((split_kernel<HD, RB, KVT, QT, NW>), grid, dim3(NW * 64), Cf::LDS, st, a);
+    hipLaunchKernelGGL((split_kernel<HD, RB, KVT, QT>), grid, dim3(Cf::NW * 64), Cf::LDS, st, a);
     return hipGetLastError();
 }
 
 template <int HD, int KVT, int QT>
 static hipError_t dispatch_rb(const SplitArgs &a, int RB, dim3 grid, hipStream_t st) {
-    constexpr int NW = HD >= 512 ? 2 : 4;
     switch (RB) {
-    case 1: return launch_split_t<HD, 1, KVT, QT, NW>(a, grid, st);
-    case 2: return launch_split_t<HD, 2, KVT, QT, NW>(a, grid, st);
-    case 3: if constexpr (HD <= 256) return launch_split_t<HD, 3, KVT, QT, NW>(a, grid, st); else return hipErrorInvalidValue;
-    case 4: if constexpr (HD <= 256) return launch_split_t<HD, 4, KVT, QT, NW>(a, grid, st); else return hipErrorInvalidValue;
+    case 1: return launch_split_t<HD, 1, KVT, QT>(a, grid, st);
+    case 2: return launch_split_t<HD, 2, KVT, QT>(a, grid, st);
+    case 3: return launch_split_t<HD, 3, KVT, QT>(a, grid, st);
+    case 4: return launch_split_t<HD, 4, KVT, QT>(a, grid, st);
     default: return hipErrorInvalidValue;
     }
 }
@@ -317,7 +382,7 @@ static hipError_t dispatch_hd(const SplitArgs &a, int RB, dim3 grid, hipStream_t
 
 static void split_tiling(const Problem &p, int &RB, int &tpb, int &nchunks) {
     const int GRP = p.NQ / p.NKV;
-    const int maxrb = p.HD >= 512 ? 2 : 4;
+    const int maxrb = 4;
     const int rows = p.T * GRP;
     RB = (rows + 15) / 16;
     if (RB > maxrb) RB = maxrb;
@@ -327,19 +392,25 @@ static void split_tiling(const Problem &p, int &RB, int &tpb, int &nchunks) {
     nchunks = (p.T + tpb - 1) / tpb;
 }
 
+size_t split_counter_count(const Problem &p) {
+    int RB, tpb, nchunks;
+    split_tiling(p, RB, tpb, nchunks);
+    return (size_t)p.nseq * nchunks * p.NKV;
+}
+
 size_t partial_rows(const Problem &p, int chunk) {
     return (size_t)p.nseq * p.T * p.NQ * (size_t)(p.max_pos / chunk + 1);
 }
 
-hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipStream_t st) {
-    if (chunk <= 0 || chunk % 32) return hipErrorInvalidValue;
+hipError_t launch_split(const Problem &p, int chunk, const Partials &part, int *counters, hipStream_t st) {
+    if (chunk <= 0 || chunk % 16) return hipErrorInvalidValue;
     if (p.NQ % p.NKV) return hipErrorInvalidValue;
     const int GRP = p.NQ / p.NKV;
     int RB, tpb, nchunks;
     split_tiling(p, RB, tpb, nchunks);
-    if (RB * 16 < GRP || RB > (p.HD >= 512 ? 2 : 4)) return hipErrorInvalidValue;
+    if (RB * 16 < GRP || RB > 4) return hipErrorInvalidValue;
     if (p.max_pos / chunk + 1 > part.ns_cap) return hipErrorInvalidValue;
-    SplitArgs a{p, part, chunk, tpb, nchunks, p.scale * kLog2e};
+    SplitArgs a{p, part, chunk, tpb, nchunks, p.scale * kLog2e, counters};
     dim3 grid(p.max_pos / chunk + 1, p.NKV, p.nseq * nchunks);
     if (grid.z > 65535u || grid.y > 65535u) return hipErrorInvalidConfiguration;
     const int kv = p.kv_dtype, q = p.q_dtype;
@@ -353,11 +424,10 @@ hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipSt
 
 hipError_t launch_combine(const Problem &p, int chunk, const Partials &part, hipStream_t st) {
     dim3 grid(p.nseq * p.T, p.NQ);
-    const int threads = p.HD >= 256 ? 256 : p.HD;
-    switch (p.o_dtype) {
-    case DT_FP32: hipLaunchKernelGGL(combine_kernel<DT_FP32>, grid, dim3(threads), 0, st, p, part, chunk); break;
-    case DT_F16: hipLaunchKernelGGL(combine_kernel<DT_F16>, grid, dim3(threads), 0, st, p, part, chunk); break;
-    case DT_BF16: hipLaunchKernelGGL(combine_kernel<DT_BF16>, grid, dim3(threads), 0, st, p, part, chunk); break;
+    switch (p.HD) {
+    case 128: hipLaunchKernelGGL(combine_kernel<128>, grid, dim3(32), 0, st, p, part, chunk); break;
+    case 256: hipLaunchKernelGGL(combine_kernel<256>, grid, dim3(64), 0, st, p, part, chunk); break;
+    case 512: hipLaunchKernelGGL(combine_kernel<512>, grid, dim3(128), 0, st, p, part, chunk); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
