@@ -143,7 +143,7 @@ Problem make_problem(const void *Q, int qt, const void *K, const void *V, int kv
 hipError_t run_split(const Problem &p, int chunk, Pool &pool, int ns_cap, hipStream_t st) {
     Partials part{pool.m, pool.l, pool.acc, ns_cap};
     // The fused combine needs one counter per (sequence, token tile, kv head); the pool holds cap of them.
-    const bool fused = split_counter_count(p) <= pool.cap && !knob_on("DGX_ATTN_UNFUSED_COMBINE");
+    const bool fused = knob_on("DGX_ATTN_FUSED_COMBINE") && split_counter_count(p) <= pool.cap;
     hipError_t e = launch_split(p, chunk, part, fused ? pool.cnt : nullptr, st);
     if (e != hipSuccess || fused) return e;
     return launch_combine(p, chunk, part, st);
@@ -204,10 +204,10 @@ hipError_t dgx_attn_decode_split(const float *Q, const void *Kc, const void *Vc,
         return launch_scalar_rows(Q, (const float *)Kc, (const float *)Vc, O, rows, NQ, NKV, HD, base, pos_step, pos_arr,
                                   kv_stride, resolve_scale(scale, HD), window, knob_on("G4_ATTN_DIAG_REVERSE") ? 1 : 0, st);
     }
-    // Rows that share one KV (kv_stride = 0) form one sequence so every K/V tile is read once for all of them.
-    const bool shared = kv_stride == 0;
-    const Problem p = make_problem(Q, DT_FP32, Kc, Vc, kv_dtype, O, DT_FP32, lse, shared ? 1 : rows, shared ? rows : 1,
-                                   NQ, NKV, HD, kv_stride, 0, base, pos_step, pos_arr, nullptr, max_pos, scale, window);
+    // Every row is its own one-token problem (KV at r * kv_stride; kv_stride = 0 re-reads one cache, mostly from
+    // L2), so a verify row runs exactly the arithmetic of the same position launched alone.
+    const Problem p = make_problem(Q, DT_FP32, Kc, Vc, kv_dtype, O, DT_FP32, lse, rows, 1, NQ, NKV, HD, kv_stride, 0,
+                                   base, pos_step, pos_arr, nullptr, max_pos, scale, window);
     return run_split(p, C, *pool, ns_cap, st);
 }
 

@@ -41,8 +41,12 @@ __device__ __forceinline__ uint16_t f32_to_op(float x, bool f16) {
     if (f16) { _Float16 h = (_Float16)x; return __builtin_bit_cast(uint16_t, h); }
     __bf16 b = (__bf16)x; return __builtin_bit_cast(uint16_t, b);
 }
+// Two floats -> one packed pair (RN-even; a single v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32 on gfx950).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 template <bool F16> __device__ __forceinline__ uint32_t pack2(float a, float b) {
-    return (uint32_t)f32_to_op(a, F16) | ((uint32_t)f32_to_op(b, F16) << 16);
+    if constexpr (F16) { const f16x2 v = {(_Float16)a, (_Float16)b}; return __builtin_bit_cast(uint32_t, v); }
+    else { const bf16x2 v = {(__bf16)a, (__bf16)b}; return __builtin_bit_cast(uint32_t, v); }
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }

@@ -50,6 +50,10 @@ __device__ __forceinline__ int win_lo(int pos, int window) {
 // the kernel also performs the LSE combine (the last workgroup of each group merges) and leaves them zero.
 hipError_t launch_split(const Problem &p, int chunk, const Partials &part, int *counters, hipStream_t st);
 size_t split_counter_count(const Problem &p);
+// Streaming decode kernel for one query token per sequence (T == 1, HD 128/256, GRP <= 16, 16-bit cache);
+// hipErrorNotSupported for other shapes. Writes chunk partials for launch_combine.
+bool decode_stream_supported(const Problem &p);
+hipError_t launch_decode_stream(const Problem &p, int chunk, const Partials &part, hipStream_t st);
 // Flash prefill kernel (waves split query rows, K/V tiles shared through LDS). kv_split = 0: one pass per row
 // tile writing O directly; kv_split > 0: keys cut at absolute multiples of kv_split, partials + combine.
 hipError_t launch_prefill(const Problem &p, int kv_split, const Partials &part, hipStream_t st);

@@ -25,6 +25,7 @@
 #include "attn_device.h"
 #include "attn_internal.h"
 #include <climits>
+#include <cstdlib>
 
 namespace dgx {
 
@@ -50,41 +51,79 @@ __device__ __forceinline__ float ld_agent(const float *p) {
 }
 __device__ __forceinline__ float ld_part(const float *p, bool agent) { return agent ? ld_agent(p) : *p; }
 
+// Wave-wide reductions over all 64 lanes (fixed xor-butterfly order, identical result in every lane).
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// LSE combine of one (row, head) by one wave, over the row's valid chunks [lo/C, pos/C]
+// (attention_decode_split.cuh:147-165): O = sum_c w_c acc_c / sum_c w_c l_c with w_c = 2^(m_c - max m).
+// Lanes load the chunk statistics in parallel (64 chunks per round), the weights are broadcast from lanes,
+// and each lane accumulates 4 head dims over the chunks in ascending order with 8 loads in flight.
+// Shared by the fused epilogue and the stand-alone combine kernel, so both give the same bits.
 template <int HD>
-__device__ __forceinline__ void combine_row4(const Problem &p, const Partials &part, int C, int s, int t, int h, int d4,
-                                             bool agent = false) {
+__device__ __forceinline__ void combine_wave(const Problem &p, const Partials &part, int C, int s, int t, int h,
+                                             bool agent) {
+    const int lane = threadIdx.x & 63;
     const int r = s * p.T + t;
     const int pos = tok_pos(p, s, t), lo = win_lo(pos, p.window);
-    const int c_lo = lo / C, c_hi = pos / C;
-    const size_t base = ((size_t)r * p.NQ + h) * part.ns_cap;
+    const int c_lo = lo / C, n = pos / C - c_lo + 1;
+    const size_t base = ((size_t)r * p.NQ + h) * part.ns_cap + c_lo;
     float mg = kNegInf;
-    for (int c = c_lo; c <= c_hi; c++) mg = fmaxf(mg, ld_part(part.m + base + c, agent));
+    for (int c0 = 0; c0 < n; c0 += 64)
+        if (c0 + lane < n) mg = fmaxf(mg, ld_part(part.m + base + c0 + lane, agent));
+    mg = wave_max(mg);
     float L = 0.f;
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (mg != kNegInf)
-        for (int c = c_lo; c <= c_hi; c++) {
-            const float mc = ld_part(part.m + base + c, agent);
-            if (mc != kNegInf) {
-                const float w = fast_exp2(mc - mg);
-                L += ld_part(part.l + base + c, agent) * w;
-                const float *pa = part.acc + (base + c) * HD + 4 * d4;
-                f32x4 v;
-                if (agent) v = f32x4{ld_agent(pa), ld_agent(pa + 1), ld_agent(pa + 2), ld_agent(pa + 3)};
-                else v = *reinterpret_cast<const f32x4 *>(pa);
-                acc += v * w;
+    for (int c0 = 0; c0 < n; c0 += 64) {
+        float x = 0.f;
+        if (c0 + lane < n && mg != kNegInf) {
+            const float mc = ld_part(part.m + base + c0 + lane, agent);
+            if (mc != kNegInf) x = ld_part(part.l + base + c0 + lane, agent) * fast_exp2(mc - mg);
+        }
+        L += wave_sum(x);
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    constexpr int D4 = HD / 4;                       // 4-dim groups of a row
+    for (int d4 = lane; d4 < D4; d4 += 64) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int c0 = 0; c0 < n; c0 += 64) {
+            float w = 0.f;
+            if (c0 + lane < n && mg != kNegInf) {
+                const float mc = ld_part(part.m + base + c0 + lane, agent);
+                if (mc != kNegInf) w = fast_exp2(mc - mg);
+            }
+            const int nn = min(64, n - c0);
+            for (int c = 0; c < nn; c += 8) {
+                f32x4 v[8];
+                float wc[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    wc[u] = __shfl(w, min(c + u, nn - 1));
+                    const float *pa = part.acc + (base + c0 + min(c + u, nn - 1)) * HD + 4 * d4;
+                    if (agent) v[u] = f32x4{ld_agent(pa), ld_agent(pa + 1), ld_agent(pa + 2), ld_agent(pa + 3)};
+                    else v[u] = *reinterpret_cast<const f32x4 *>(pa);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (c + u < nn && wc[u] != 0.f) acc += v[u] * wc[u];
             }
         }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    const f32x4 o = acc * inv;
-    const size_t oi = ((size_t)r * p.NQ + h) * HD + 4 * d4;
-    if (p.o_dtype == DT_FP32) *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.O) + oi) = o;
-    else {
-        const bool f16 = p.o_dtype == DT_F16;
-        const u32x2 w = u32x2{(uint32_t)f32_to_op(o.x, f16) | ((uint32_t)f32_to_op(o.y, f16) << 16),
-                              (uint32_t)f32_to_op(o.z, f16) | ((uint32_t)f32_to_op(o.w, f16) << 16)};
-        *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(p.O) + oi) = w;
+        const f32x4 o = acc * inv;
+        const size_t oi = ((size_t)r * p.NQ + h) * HD + 4 * d4;
+        if (p.o_dtype == DT_FP32) *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.O) + oi) = o;
+        else {
+            const bool f16 = p.o_dtype == DT_F16;
+            const u32x2 ow = u32x2{(uint32_t)f32_to_op(o.x, f16) | ((uint32_t)f32_to_op(o.y, f16) << 16),
+                                   (uint32_t)f32_to_op(o.z, f16) | ((uint32_t)f32_to_op(o.w, f16) << 16)};
+            *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(p.O) + oi) = ow;
+        }
     }
-    if (p.lse && d4 == 0) p.lse[(size_t)r * p.NQ + h] = (L > 0.f) ? (mg + log2f(L)) * kLn2 : kNegInf;
+    if (p.lse && lane == 0) p.lse[(size_t)r * p.NQ + h] = (L > 0.f) ? (mg + log2f(L)) * kLn2 : kNegInf;
 }
 
 template <int HD, int RB>
@@ -101,8 +140,18 @@ struct SplitCfg {
     static_assert(CPT >= 1 && (KT * HD / 8) % (NW * 64) == 0, "tile chunks");
 };
 
+#ifdef DGX_TRACE
+__device__ unsigned long long g_trace[1 << 16][4];
+extern "C" hipError_t dgx_trace_read(void *host, size_t bytes) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif
+
 template <int HD, int RB, int KVT, int QT>
 __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
+#ifdef DGX_TRACE
+    const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
+#endif
     using Cf = SplitCfg<HD, RB>;
     constexpr int NW = Cf::NW;
     constexpr bool F16 = OpIsF16<KVT>::value;
@@ -111,7 +160,9 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
 
     const Problem &p = a.p;
-    const int c = blockIdx.x, kvh = blockIdx.y;
+    // blockIdx.x = kv head (fastest), so the NKV workgroups of one key chunk are dispatched together and read the
+    // interleaved head slices of the same cache rows at the same time.
+    const int kvh = blockIdx.x, c = blockIdx.y;
     const int seq = blockIdx.z / a.nchunks, tchunk = blockIdx.z % a.nchunks;
     const int GRP = p.NQ / p.NKV;
     const int tok0 = tchunk * a.tpb, tok1 = min(p.T, tok0 + a.tpb);
@@ -198,7 +249,7 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
     const int jb = (j_lo / Cf::KT) * Cf::KT;
     const int ntile = (j_hi - jb + Cf::KT - 1) / Cf::KT;
     fetch(kr0, vr0, jb);
-    if (ntile > 1) fetch(kr1, vr1, jb + Cf::KT);
+    fetch(kr1, vr1, jb + Cf::KT);
     stash(kr0, vr0, 0);
     __syncthreads();                                           // Q rows and tile 0 are in LDS
     constexpr bool QREG = RB * Cf::KS <= 8;                    // Q fragments in registers when they fit
@@ -276,18 +327,35 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
         }
     };
     // Iteration it: fetch tile it+2 into the register stage that held tile it, compute tile it from LDS, stash
-    // tile it+1 (fetched one iteration earlier) into the other LDS buffer, barrier.
-    for (int it = 0; it < ntile; it += 2) {
-        if (it + 2 < ntile) fetch(kr0, vr0, jb + Cf::KT * (it + 2));
+    // tile it+1 (fetched one iteration earlier) into the other LDS buffer, barrier. Fetches and stashes are
+    // unconditional (past the last tile a fetch re-reads the last key row, an L2 hit, and a stash fills a buffer
+    // that is never read again) so that every wait before a stash sees exactly the newer tile's loads in flight
+    // and the compiler never has to drain the pipeline at a control-flow merge.
+    int it = 0;
+    for (; it + 1 < ntile; it += 2) {
+        fetch(kr0, vr0, jb + Cf::KT * (it + 2));
         compute(it);
-        if (it + 1 < ntile) stash(kr1, vr1, 1);
+        stash(kr1, vr1, 1);
         __syncthreads();
-        if (it + 1 >= ntile) break;
-        if (it + 3 < ntile) fetch(kr1, vr1, jb + Cf::KT * (it + 3));
+        fetch(kr1, vr1, jb + Cf::KT * (it + 3));
         compute(it + 1);
-        if (it + 2 < ntile) stash(kr0, vr0, 0);
+        stash(kr0, vr0, 0);
         __syncthreads();
     }
+    if (it < ntile) compute(it);                                // odd tile count: the last tile sits in buffer 0
+#ifdef DGX_TRACE
+    if (tid == 0) {
+        const size_t bid = ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        unsigned xcc, hwid;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
+        xcc = (xcc & 0xf) | (((hwid >> 8) & 0xf) << 4) | (((hwid >> 12) & 0x7) << 8);   // xcc | cu << 4 | sh,se << 8
+        g_trace[bid & 0xffff][0] = t_start;
+        g_trace[bid & 0xffff][1] = __builtin_amdgcn_s_memrealtime();
+        g_trace[bid & 0xffff][2] = ntile;
+        g_trace[bid & 0xffff][3] = xcc;
+    }
+#endif
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) l[rb] = sum_over_groups(l[rb]);
 
@@ -325,23 +393,24 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
     if (threadIdx.x == 0) {
         // Chunks that exist in the grid and intersect the group's key range (a max_pos below the true positions
         // drops keys, as in the reference, but keeps the counters consistent).
-        const int expected = min((hi_b - 1) / C, (int)gridDim.x - 1) - lo_b / C + 1;
+        const int expected = min((hi_b - 1) / C, (int)gridDim.y - 1) - lo_b / C + 1;
         const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = (old == expected - 1);
         if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!s_last) return;
-    for (int idx = threadIdx.x; idx < nrows * (HD / 4); idx += NW * 64)
-        combine_row4<HD>(p, a.part, C, seq, tok0 + (idx / (HD / 4)) / GRP, kvh * GRP + (idx / (HD / 4)) % GRP, idx % (HD / 4),
-                         true);
+    for (int row = wave; row < nrows; row += NW)
+        combine_wave<HD>(p, a.part, C, seq, tok0 + row / GRP, kvh * GRP + row % GRP, true);
 }
 
-// Stand-alone LSE combine (one workgroup per (row, head)); used when no arrival counters are supplied.
+// Stand-alone LSE combine: one wave per (row, head); used when no arrival counters are supplied.
 template <int HD>
 __global__ void __launch_bounds__(256) combine_kernel(const Problem p, const Partials part, int C) {
-    const int r = blockIdx.x, h = blockIdx.y;
-    for (int d4 = threadIdx.x; d4 < HD / 4; d4 += blockDim.x) combine_row4<HD>(p, part, C, r / p.T, r % p.T, h, d4);
+    const int rh = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (rh >= p.nseq * p.T * p.NQ) return;
+    const int r = rh / p.NQ, h = rh % p.NQ;
+    combine_wave<HD>(p, part, C, r / p.T, r % p.T, h, false);
 }
 
 // ---------------------------------------------------------------- host side
@@ -404,6 +473,10 @@ size_t partial_rows(const Problem &p, int chunk) {
 
 hipError_t launch_split(const Problem &p, int chunk, const Partials &part, int *counters, hipStream_t st) {
     if (chunk <= 0 || chunk % 16) return hipErrorInvalidValue;
+    // Opt-in: the LDS-free streaming decode kernel (measured slower than the LDS-staged path on the B=16 ragged
+    // workload, kept for tuning).
+    if (!counters && decode_stream_supported(p) && getenv("DGX_ATTN_DECODE_STREAM"))
+        return launch_decode_stream(p, chunk, part, st);
     if (p.NQ % p.NKV) return hipErrorInvalidValue;
     const int GRP = p.NQ / p.NKV;
     int RB, tpb, nchunks;
@@ -411,7 +484,7 @@ hipError_t launch_split(const Problem &p, int chunk, const Partials &part, int *
     if (RB * 16 < GRP || RB > 4) return hipErrorInvalidValue;
     if (p.max_pos / chunk + 1 > part.ns_cap) return hipErrorInvalidValue;
     SplitArgs a{p, part, chunk, tpb, nchunks, p.scale * kLog2e, counters};
-    dim3 grid(p.max_pos / chunk + 1, p.NKV, p.nseq * nchunks);
+    dim3 grid(p.NKV, p.max_pos / chunk + 1, p.nseq * nchunks);
     if (grid.z > 65535u || grid.y > 65535u) return hipErrorInvalidConfiguration;
     const int kv = p.kv_dtype, q = p.q_dtype;
     if (kv == DT_F16 && q == DT_FP32) return dispatch_hd<DT_F16, DT_FP32>(a, RB, grid, st);
@@ -423,11 +496,12 @@ hipError_t launch_split(const Problem &p, int chunk, const Partials &part, int *
 }
 
 hipError_t launch_combine(const Problem &p, int chunk, const Partials &part, hipStream_t st) {
-    dim3 grid(p.nseq * p.T, p.NQ);
+    const int rows = p.nseq * p.T * p.NQ;
+    dim3 grid((rows + 3) / 4);
     switch (p.HD) {
-    case 128: hipLaunchKernelGGL(combine_kernel<128>, grid, dim3(32), 0, st, p, part, chunk); break;
-    case 256: hipLaunchKernelGGL(combine_kernel<256>, grid, dim3(64), 0, st, p, part, chunk); break;
-    case 512: hipLaunchKernelGGL(combine_kernel<512>, grid, dim3(128), 0, st, p, part, chunk); break;
+    case 128: hipLaunchKernelGGL(combine_kernel<128>, grid, dim3(256), 0, st, p, part, chunk); break;
+    case 256: hipLaunchKernelGGL(combine_kernel<256>, grid, dim3(256), 0, st, p, part, chunk); break;
+    case 512: hipLaunchKernelGGL(combine_kernel<512>, grid, dim3(256), 0, st, p, part, chunk); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
