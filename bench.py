@@ -159,7 +159,7 @@ def cpu_baseline(w):
 
 def traffic_from_profile():
     """HBM bytes per launch of the decode kernel from the committed rocprofv3 PMC summary, if present."""
-    path = os.path.join(ROOT, "profiles", "decode_split_b16_pmc.txt")
+    path = os.path.join(ROOT, "profiles", "decode_split_b16.md")
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -175,6 +175,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["decode", "prefill", "all"], default="all")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a plain 1 GiB device copy (scale reference for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (requested --gpus {args.gpus}).",
@@ -183,6 +185,12 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     A.lib()
     out = {}
+    if args.calib_copy:
+        src = torch.empty(1 << 28, device="cuda", dtype=torch.float32).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     w = decode_workload()
     ms, nbytes = run_decode(w, args.steps, args.warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9

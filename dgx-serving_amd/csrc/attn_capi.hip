@@ -220,6 +220,13 @@ hipError_t dgx_flash_attn_reserve(int Sq, int NQ, int base, int HD) {
     return pool_grow(*pool, (size_t)Sq * NQ * ns, (size_t)HD);
 }
 
+hipError_t dgx_flash_attn_reserve_partials(size_t partials, int hd_max) {
+    if (hd_max <= 0 || hd_max > 512) return hipErrorInvalidValue;
+    Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(g_pool_mu);
+    return pool_grow(*pool, partials, (size_t)hd_max);
+}
+
 hipError_t dgx_flash_attn(const float *Q, const void *Kc, const void *Vc, int kv_dtype, float *O, float *lse,
                           int Sq, int NQ, int NKV, int HD, int base, hipStream_t st, const unsigned *anc,
                           float scale, int window) {

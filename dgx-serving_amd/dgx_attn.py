@@ -35,6 +35,7 @@ def lib():
             "dgx_attn_decode_split": ([P, P, P, I, P, P, I, I, I, I, I, I, P, I, L64, I, P, F, I], I),
             "dgx_flash_attn": ([P, P, P, I, P, P, I, I, I, I, I, P, P, F, I], I),
             "dgx_flash_attn_reserve": ([I, I, I, I], I),
+            "dgx_flash_attn_reserve_partials": ([S, I], I),
             "dgx_flash_attn_v2": ([P, P, P, I, P, P, I, I, I, I, I, P, F, I, I], I),
             "dgx_attn": ([P, P, P, P, I, I, I, I, P, F, I], I),
             "dgx_attn_decode": ([P, P, P, P, I, I, I, I, I, P, F, I], I),

@@ -73,6 +73,9 @@ hipError_t dgx_flash_attn(const float *Q, const void *Kc, const void *Vc, int kv
                           float scale, int window);
 /* Pre-size the flash scratch for Sq tokens at base. Replaces reserve_flash_attn_scratch(), attention_flash.cuh:236. */
 hipError_t dgx_flash_attn_reserve(int Sq, int NQ, int base, int HD);
+/* Pre-size the flash scratch to `partials` (row, head, split) partials of hd_max floats, the reference's own
+ * unit. Replaces reserve_flash_attn_scratch(need, hd), attention_flash.cuh:236-252. */
+hipError_t dgx_flash_attn_reserve_partials(size_t partials, int hd_max);
 
 /* Prefill / chunked prefill (base > 0 = chunk over a cached prefix). f16_mma: operand precision request of the
  * reference; here the MFMA operand format always follows the cache (f16 cache: f16, bf16/fp32 cache: bf16).

@@ -1,0 +1,130 @@
+// dgx_attn.hpp - the reference's C++ attention launch surface over the MI355X C ABI (dgx_attn.h).
+//
+// Callers of hyunlord/dgx-serving (models/*.cu, tests/test_attn_*.cu) include this header in place of
+// kernels/attention.cuh, attention_decode_split.cuh, attention_flash.cuh, attention_flash_v2.cuh and
+// kv_store.cuh and compile unchanged apart from the CUDA -> HIP type names (cudaStream_t -> hipStream_t,
+// __nv_bfloat16 -> __hip_bfloat16). Every wrapper keeps the reference's name, argument order, defaults and error
+// convention (fprintf to stderr, then abort(); an invalid knob exits 1). All kernels live in libdgx_attn.so.
+#ifndef DGX_ATTN_HPP
+#define DGX_ATTN_HPP
+#include <cstddef>
+#include <cstdio>
+#include <cstdlib>
+#include <type_traits>
+#include <hip/hip_runtime_api.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include "dgx_attn.h"
+
+enum { KV_FP32 = DGX_DT_FP32, KV_F16 = DGX_DT_F16, KV_BF16 = DGX_DT_BF16 };   // kernels/kv_store.cuh:20
+
+namespace dgx_detail {
+inline void check(hipError_t e, const char *who) {
+    if (e != hipSuccess) {
+        fprintf(stderr, "[%s] failed: %s\n", who, hipGetErrorString(e));
+        abort();
+    }
+}
+template <class KV> constexpr int kv_code() {
+    static_assert(std::is_same<KV, float>::value || std::is_same<KV, __half>::value ||
+                      std::is_same<KV, __hip_bfloat16>::value,
+                  "unsupported KV type");
+    return std::is_same<KV, float>::value ? KV_FP32 : (std::is_same<KV, __half>::value ? KV_F16 : KV_BF16);
+}
+}  // namespace dgx_detail
+
+// ---- kernels/kv_store.cuh:25-113
+inline int g4_kv_dtype() {
+    const int d = dgx_kv_dtype();
+    if (d < 0) exit(1);                         // the reference exits on an invalid G4_KV_DTYPE (kv_store.cuh:36)
+    return d;
+}
+inline void g4_kv_force_fp32(const char *why) { dgx_kv_force_fp32(why); }
+static inline size_t g4_kv_elem() { return g4_kv_dtype() == KV_FP32 ? 4 : 2; }
+// Byte-offset arithmetic on float* cache handles whatever the storage dtype (kv_store.cuh:47-50).
+template <class P> static inline P *kv_at(P *p, size_t elems) {
+    using B = typename std::conditional<std::is_const<P>::value, const char, char>::type;
+    return reinterpret_cast<P *>(reinterpret_cast<B *>(p) + elems * g4_kv_elem());
+}
+static inline void kv_store(const float *src, float *dst, size_t n, int which, hipStream_t st = 0) {
+    dgx_detail::check(dgx_kv_store(src, dst, n, g4_kv_dtype(), which, st), "kv_store");
+}
+
+// ---- kernels/attention.cuh:72-198 (fp32 caches)
+static inline void launch_attn(const float *Q, const float *K, const float *V, float *O, int S, int NQ, int NKV, int HD,
+                               hipStream_t st = 0, float scale = 0.f, int window = 0) {
+    dgx_detail::check(dgx_attn(Q, K, V, O, S, NQ, NKV, HD, st, scale, window), "attn");
+}
+static inline void launch_attn_decode(const float *Q, const float *Kc, const float *Vc, float *O, int Sq, int NQ,
+                                      int NKV, int HD, int base, hipStream_t st = 0, float scale = 0.f,
+                                      int window = 0) {
+    dgx_detail::check(dgx_attn_decode(Q, Kc, Vc, O, Sq, NQ, NKV, HD, base, st, scale, window), "attn_decode");
+}
+static inline void launch_attn_decode_batch(const float *Q, const float *Kc, const float *Vc, float *O, int B, int NQ,
+                                            int NKV, int HD, int base, long kv_stride, hipStream_t st = 0,
+                                            float scale = 0.f, int window = 0, const int *base_b = nullptr) {
+    dgx_detail::check(dgx_attn_decode_batch(Q, Kc, Vc, O, B, NQ, NKV, HD, base, kv_stride, st, scale, window, base_b),
+                      "attn_decode_batch");
+}
+
+// ---- kernels/attention_decode_split.cuh:26-231 (cache dtype from g4_kv_dtype(), float* handles)
+static inline int attn_split_chunk() {
+    const int c = dgx_attn_split_chunk();
+    if (c < 0) exit(1);
+    return c;
+}
+static inline int attn_split_ns_cap(int max_len) { const int C = attn_split_chunk(); return (max_len + C - 1) / C; }
+static inline void attn_split_reserve(int rows, int NQ, int max_len, int hd_max) {
+    dgx_detail::check(dgx_attn_split_reserve(rows, NQ, max_len, hd_max), "attn_split reserve");
+}
+static inline void launch_attn_decode_split(const float *Q, const float *Kc, const float *Vc, float *O, int rows,
+                                            int NQ, int NKV, int HD, int base, int pos_step, const int *pos_arr,
+                                            int max_pos, long kv_stride, int ns_cap, hipStream_t st = 0,
+                                            float scale = 0.f, int window = 0) {
+    dgx_detail::check(dgx_attn_decode_split(Q, Kc, Vc, g4_kv_dtype(), O, nullptr, rows, NQ, NKV, HD, base, pos_step,
+                                            pos_arr, max_pos, kv_stride, ns_cap, st, scale, window),
+                      "attn_split");
+}
+
+// ---- kernels/attention_flash.cuh:236-306 (typed caches)
+static inline void reserve_flash_attn_scratch(size_t need, size_t hd) {
+    dgx_detail::check(dgx_flash_attn_reserve_partials(need, (int)hd), "flash_attn reserve");
+}
+template <int HD, int BC, int NW, typename KV>
+static inline void launch_flash_attn2bs(const float *Q, const KV *Kc, const KV *Vc, float *O, int Sq, int NQ, int NKV,
+                                        int base, hipStream_t st = 0, const unsigned *anc = nullptr,
+                                        float scale = 0.f, int window = 0) {
+    static_assert(HD == 128 || HD == 256 || HD == 512, "unsupported head_dim");
+    (void)BC; (void)NW;                                  // tile shape is chosen by the gfx950 kernels
+    dgx_detail::check(dgx_flash_attn(Q, Kc, Vc, dgx_detail::kv_code<KV>(), O, nullptr, Sq, NQ, NKV, HD, base, st, anc,
+                                     scale, window),
+                      "flash_attn");
+}
+template <typename KV>
+static inline void launch_flash_attn(const float *Q, const KV *Kc, const KV *Vc, float *O, int Sq, int NQ, int NKV,
+                                     int HD, int base, hipStream_t st = 0, const unsigned *anc = nullptr,
+                                     float scale = 0.f, int window = 0) {
+    if (HD != 128 && HD != 256 && HD != 512) {
+        fprintf(stderr, "[flash_attn] unsupported head_dim=%d (128/256/512 only)\n", HD);
+        abort();
+    }
+    dgx_detail::check(dgx_flash_attn(Q, Kc, Vc, dgx_detail::kv_code<KV>(), O, nullptr, Sq, NQ, NKV, HD, base, st, anc,
+                                     scale, window),
+                      "flash_attn");
+}
+
+// ---- kernels/attention_flash_v2.cuh:284-292
+template <typename KV>
+static inline void launch_flash_attn_v2(const float *Q, const KV *Kc, const KV *Vc, float *O, int Sq, int NQ, int NKV,
+                                        int HD, int base, hipStream_t st = 0, float scale = 0.f, int window = 0,
+                                        bool f16_mma = false) {
+    if (HD != 256 && HD != 512 && HD != 128) {
+        fprintf(stderr, "[flash_v2] unsupported head_dim=%d (128/256/512 only)\n", HD);
+        abort();
+    }
+    dgx_detail::check(dgx_flash_attn_v2(Q, Kc, Vc, dgx_detail::kv_code<KV>(), O, nullptr, Sq, NQ, NKV, HD, base, st,
+                                        scale, window, f16_mma ? 1 : 0),
+                      "flash_v2");
+}
+
+#endif  // DGX_ATTN_HPP
