@@ -196,7 +196,7 @@ def main():
     gbs = nbytes / (ms * 1e-3) / 1e9
     extra = {}
     if args.only in ("prefill", "all"):
-        pms, pflops = run_prefill(args.steps, args.warmup, kv_split=int(os.environ.get("BENCH_PREFILL_SPLIT", "256")))
+        pms, pflops = run_prefill(args.steps, args.warmup, kv_split=int(os.environ.get("BENCH_PREFILL_SPLIT", "0")))
         ptf = pflops / (pms * 1e-3) / 1e12
         extra["prefill_causal_T1024"] = dict(us=round(pms * 1e3, 2), tflops=round(ptf, 2),
                                              frac_bf16_peak=round(ptf / BF16_PEAK_TFLOPS, 4))

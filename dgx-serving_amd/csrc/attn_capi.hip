@@ -122,9 +122,6 @@ bool valid_dtype(int d) { return d == DT_FP32 || d == DT_F16 || d == DT_BF16; }
 
 // Flash-path split size for short query runs (the reference's FD_SPLIT_KV, attention_flash.cuh:11).
 constexpr int kFlashChunk = 512;
-// Key split of the prefill kernel in the drop-in flash entry points: a fixed absolute boundary, so a prompt's
-// result does not depend on how it is chunked.
-constexpr int kPrefillSplit = 512;
 // Query tokens up to which dgx_flash_attn runs the split kernel (decode, verify, trees of <= 32 nodes).
 constexpr int kFlashShortSq = 32;
 
@@ -213,9 +210,10 @@ hipError_t dgx_attn_decode_split(const float *Q, const void *Kc, const void *Vc,
 
 hipError_t dgx_flash_attn_reserve(int Sq, int NQ, int base, int HD) {
     if (Sq < 0 || NQ <= 0 || base < 0 || !valid_hd(HD)) return hipErrorInvalidValue;
+    // Long query runs use the prefill kernel without key splits and need no scratch.
+    if (Sq > kFlashShortSq) return hipSuccess;
     Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
-    const int C = Sq <= kFlashShortSq ? kFlashChunk : kPrefillSplit;
-    const size_t ns = (size_t)(base + Sq) / C + 1;
+    const size_t ns = (size_t)(base + Sq) / kFlashChunk + 1;
     std::lock_guard<std::mutex> lock(g_pool_mu);
     return pool_grow(*pool, (size_t)Sq * NQ * ns, (size_t)HD);
 }
@@ -246,8 +244,10 @@ hipError_t dgx_flash_attn(const float *Q, const void *Kc, const void *Vc, int kv
         const int ns = (base + Sq - 1) / kFlashChunk + 1;
         return run_split(p, kFlashChunk, *pool, ns, st);
     }
-    Partials part{pool->m, pool->l, pool->acc, (base + Sq - 1) / kPrefillSplit + 1};
-    return launch_prefill(p, kPrefillSplit, part, st);
+    if (anc) return hipErrorInvalidValue;      // a tree mask covers at most 32 nodes (attention_flash.cuh:177)
+    // No key split: the prefill kernel balances causal work by pairing query tiles, and a row's result does not
+    // depend on how the prompt is chunked.
+    return launch_prefill(p, 0, Partials{nullptr, nullptr, nullptr, 0}, st);
 }
 
 hipError_t dgx_flash_attn_v2(const float *Q, const void *Kc, const void *Vc, int kv_dtype, float *O, float *lse,
@@ -258,17 +258,9 @@ hipError_t dgx_flash_attn_v2(const float *Q, const void *Kc, const void *Vc, int
     if (!Q || !Kc || !Vc || !O || Sq < 0 || base < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || !valid_hd(HD) ||
         !valid_dtype(kv_dtype))
         return hipErrorInvalidValue;
-    Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
-    const int ns = (base + Sq - 1) / kPrefillSplit + 1;
-    {
-        std::lock_guard<std::mutex> lock(g_pool_mu);
-        e = pool_grow(*pool, (size_t)Sq * NQ * ns, (size_t)HD);
-        if (e != hipSuccess) return e;
-    }
     const Problem p = make_problem(Q, DT_FP32, Kc, Vc, kv_dtype, O, DT_FP32, lse, 1, Sq, NQ, NKV, HD, 0, 1, base, 1,
                                    nullptr, nullptr, base + Sq - 1, scale, window);
-    Partials part{pool->m, pool->l, pool->acc, ns};
-    return launch_prefill(p, kPrefillSplit, part, st);
+    return launch_prefill(p, 0, Partials{nullptr, nullptr, nullptr, 0}, st);
 }
 
 hipError_t dgx_attn(const float *Q, const float *K, const float *V, float *O, int S, int NQ, int NKV, int HD,
@@ -330,7 +322,7 @@ hipError_t dgx_attn_prefill(const void *Q, int q_dtype, const void *Kc, const vo
     if (nseq == 0 || Sq == 0) return hipSuccess;
     if (!Q || !Kc || !Vc || !O || nseq < 0 || Sq < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || !valid_hd(HD) ||
         max_pos < 0 || !valid_dtype(q_dtype) || !valid_dtype(o_dtype) || !valid_dtype(kv_dtype) || kv_split < 0 ||
-        kv_split % 32)
+        kv_split % 64)
         return hipErrorInvalidValue;
     Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
     const int ns = kv_split > 0 ? max_pos / kv_split + 1 : 1;

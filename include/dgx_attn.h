@@ -116,7 +116,7 @@ hipError_t dgx_attn_batch(const void *Q, int q_dtype, const void *Kc, const void
                           int o_dtype, float *lse, int B, int Tq, int NQ, int NKV, int HD, const int *base_b, int base,
                           long kv_stride, const unsigned *anc, int max_pos, int chunk, hipStream_t st, float scale,
                           int window);
-/* Prefill with explicit key split (kv_split = 0: none; else a multiple of 32, partials + combine for rows that
+/* Prefill with explicit key split (kv_split = 0: none; else a multiple of 64, partials + combine for rows that
  * span splits) over nseq sequences of Sq tokens at (base_b ? base_b[s] : base) + i. Uses the flash scratch
  * (grown in the call when needed). Native form of launch_flash_attn_v2 (attention_flash_v2.cuh:284-292). */
 hipError_t dgx_attn_prefill(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
