@@ -56,13 +56,20 @@ def decode_workload(seed=2026):
     return dict(B=B, NQ=NQ, NKV=NKV, HD=HD, ML=ML, lens=lens, K=K, V=V, Q=Q, O=O, pos=pos)
 
 
-def run_decode(w, steps, warmup, chunk=512):
+def run_decode(w, steps, warmup, chunk=512, copies=1):
     B, NQ, NKV, HD, ML = w["B"], w["NQ"], w["NKV"], w["HD"], w["ML"]
     max_pos = int(w["lens"].max()) - 1
     # the reservation is sized at the library's default chunk; smaller chunks need proportionally more partials
     A.split_reserve(B * max(1, -(-A.split_chunk() // chunk)), NQ, ML, HD)
-    fn = lambda: A.attn_batch(w["Q"], w["K"], w["V"], w["O"], B, 1, NQ, NKV, HD, w["pos"], ML * NKV * HD, max_pos,
-                              chunk=chunk)
+    kvs = [(w["K"], w["V"])]
+    for i in range(1, copies):
+        kvs.append((torch.randn_like(w["K"]) * 0.5, torch.randn_like(w["V"]) * 0.5))
+    it = [0]
+
+    def fn():
+        K, V = kvs[it[0] % len(kvs)]
+        it[0] += 1
+        A.attn_batch(w["Q"], K, V, w["O"], B, 1, NQ, NKV, HD, w["pos"], ML * NKV * HD, max_pos, chunk=chunk)
     ms = timed(fn, steps, warmup)
     nbytes = int(w["lens"].sum()) * NKV * HD * 2 * 2 + 2 * B * NQ * HD * 2
     return ms, nbytes
@@ -192,7 +199,8 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
     w = decode_workload()
-    ms, nbytes = run_decode(w, args.steps, args.warmup)
+    ms, nbytes = run_decode(w, args.steps, args.warmup, chunk=int(os.environ.get("BENCH_DECODE_CHUNK", "512")),
+                           copies=int(os.environ.get("BENCH_DECODE_COPIES", "3")))
     gbs = nbytes / (ms * 1e-3) / 1e9
     extra = {}
     if args.only in ("prefill", "all"):

@@ -77,7 +77,6 @@ bool knob_on(const char *name) { const char *v = knob_raw(name); return v && v[0
 constexpr int kMaxDev = 64;
 struct Pool {
     float *m = nullptr, *l = nullptr, *acc = nullptr;
-    int *cnt = nullptr;                // arrival counters of the fused combine (zeroed once, self-resetting)
     size_t cap = 0, acc_cap = 0;
 };
 Pool g_split[kMaxDev], g_flash[kMaxDev];
@@ -89,12 +88,8 @@ hipError_t pool_grow(Pool &p, size_t need, size_t hd) {
         if (p.m) { hipError_t e = hipFree(p.m); if (e != hipSuccess) return e; p.m = nullptr; }
         if (p.l) { hipError_t e = hipFree(p.l); if (e != hipSuccess) return e; p.l = nullptr; }
         p.cap = 0;
-        if (p.cnt) { hipError_t e = hipFree(p.cnt); if (e != hipSuccess) return e; p.cnt = nullptr; }
         hipError_t e = hipMalloc(&p.m, need * sizeof(float)); if (e != hipSuccess) return e;
         e = hipMalloc(&p.l, need * sizeof(float)); if (e != hipSuccess) return e;
-        e = hipMalloc(&p.cnt, need * sizeof(int)); if (e != hipSuccess) return e;
-        e = hipMemset(p.cnt, 0, need * sizeof(int)); if (e != hipSuccess) return e;
-        e = hipDeviceSynchronize(); if (e != hipSuccess) return e;
         p.cap = need;
     }
     if (p.acc_cap < need * hd) {
@@ -139,10 +134,8 @@ Problem make_problem(const void *Q, int qt, const void *K, const void *V, int kv
 
 hipError_t run_split(const Problem &p, int chunk, Pool &pool, int ns_cap, hipStream_t st) {
     Partials part{pool.m, pool.l, pool.acc, ns_cap};
-    // The fused combine needs one counter per (sequence, token tile, kv head); the pool holds cap of them.
-    const bool fused = knob_on("DGX_ATTN_FUSED_COMBINE") && split_counter_count(p) <= pool.cap;
-    hipError_t e = launch_split(p, chunk, part, fused ? pool.cnt : nullptr, st);
-    if (e != hipSuccess || fused) return e;
+    hipError_t e = launch_split(p, chunk, part, st);
+    if (e != hipSuccess) return e;
     return launch_combine(p, chunk, part, st);
 }
 

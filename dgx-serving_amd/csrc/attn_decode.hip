@@ -1,22 +1,27 @@
 // Streaming split-KV GQA decode on gfx950: one query token per sequence, HD 128 or 256, up to 16 q-heads per KV
-// head (the decode rows of kernels/attention_decode_split.cuh:43-145 and of the per-slot flash decode at
-// models/qwen35_batch.cu:165-167).
+// head, 16-bit caches (the decode rows of kernels/attention_decode_split.cuh:43-145 and of the per-slot flash
+// decode at models/qwen35_batch.cu:165-167).
 //
-// Grid: (kv head, key chunk of C keys, sequence). A workgroup owns the GRP query rows of one KV head and one
-// chunk; its 4 wave64s take the chunk's 16-key tiles round-robin (wave w: tiles w, w+4, ...) and run fully
-// independent online softmaxes, merged in wave order at the end. The main loop touches no LDS and has no
-// barrier:
-//   * K is read straight into MFMA A fragments (lane = key, 16 bytes of head dims per load),
-//   * S^T = K Q^T on 16x16x32 MFMA (Q fragments come from LDS, staged once),
-//   * V rows are read coalesced, staged in the wave's private LDS slice and read back with the gfx950 transpose
-//     read (ds_read_b64_tr_b16) as the A fragments of O^T += V^T P^T on 16x16x16 MFMA; P^T comes straight from
-//     the softmax registers. LDS carries 16 KB per 16-key tile and wave (V in and out) and needs no barrier.
+// Grid: one workgroup per (sequence, key chunk of C keys, kv head) that holds keys, enumerated on the device from
+// the positions, so the launched workgroups with work come first and spread over all CUs. A workgroup owns the
+// GRP query rows of one KV head and one chunk; its NW wave64s take the chunk's 16-key tiles round-robin (wave w:
+// tiles w, w+NW, ...) and run fully independent online softmaxes, merged in wave order at the end. The main loop
+// has no workgroup barrier:
+//   * K and V rows are streamed from HBM with 16-byte non-temporal loads, whole 512-byte head rows per half
+//     wave (the KV cache is read once per call: non-temporal loads sustain a higher HBM rate and leave the
+//     caches to the partials and Q),
+//   * the K tile passes through the wave's private LDS slice into MFMA A fragments (lane = key),
+//     S^T = K Q^T on 16x16x32 MFMA (Q fragments come from LDS, staged once),
+//   * the V tile lands in the same slice and is read back with the gfx950 transpose read (ds_read_b64_tr_b16)
+//     as the A fragments of O^T += V^T P^T on 16x16x16 MFMA; P^T comes straight from the softmax registers.
 //
 // Chunk boundaries and tile positions are absolute and the wave that owns a tile depends only on its position,
 // so a row's result is identical whatever the batch, grid or maximum position (batch row == single row).
 #include "attn_device.h"
 #include "attn_internal.h"
 #include <climits>
+#include <cstdlib>
+
 
 namespace dgx {
 
@@ -27,9 +32,9 @@ struct DecodeArgs {
     float sl2;
 };
 
-template <int HD>
+template <int HD, int NW_>
 struct DecodeCfg {
-    static constexpr int NW = 4, KT = 16;
+    static constexpr int NW = NW_, KT = 16;
     static constexpr int KS = HD / 32;                 // 32-dim blocks (QK k-steps, V fragment loads)
     static constexpr int DB = HD / 16;                 // 16-dim output blocks
     static constexpr int QSTR = HD + 8;                // Q row stride in LDS (16-bit elements)
@@ -37,28 +42,24 @@ struct DecodeCfg {
     static constexpr int VSTR = HD + 8;                // V tile row stride in LDS (16-bit elements)
     static constexpr int VCH = KT * HD / 8 / 64;       // 16-byte V chunks per lane per tile
     static constexpr size_t LDS_Q = (size_t)16 * QSTR * 2;
-    static constexpr size_t LDS_V = (size_t)NW * KT * VSTR * 2;     // one private V tile per wave
+    static constexpr size_t LDS_V = (size_t)NW * KT * VSTR * 2;     // one private tile per wave (K, then V)
     static constexpr size_t LDS_MERGE = ((size_t)2 * NW * 16 + (size_t)16 * BSTR) * 4;
     static constexpr size_t LDS = LDS_Q + (LDS_V > LDS_MERGE ? LDS_V : LDS_MERGE);
 };
 
 #ifdef DGX_TRACE
 __device__ unsigned long long g_dtrace[1 << 16][4];
-__device__ unsigned long long g_ptrace[64][16][5];   // [wave slot][tile][phase] shader-clock stamps
 extern "C" hipError_t dgx_dtrace_read(void *host, size_t bytes) {
     return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dtrace), bytes, 0, hipMemcpyDeviceToHost);
 }
-extern "C" hipError_t dgx_ptrace_read(void *host, size_t bytes) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_ptrace), bytes, 0, hipMemcpyDeviceToHost);
-}
 #endif
 
-template <int HD, int KVT, int QT>
-__global__ void __launch_bounds__(256) decode_stream_kernel(const DecodeArgs a) {
+template <int HD, int NW_, int KVT, int QT>
+__global__ void __launch_bounds__(NW_ * 64) decode_stream_kernel(const DecodeArgs a) {
 #ifdef DGX_TRACE
     const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
 #endif
-    using Cf = DecodeCfg<HD>;
+    using Cf = DecodeCfg<HD, NW_>;
     constexpr int NW = Cf::NW, KT = Cf::KT;
     constexpr bool F16 = OpIsF16<KVT>::value;
     using KE = typename Elem<KVT>::T;
@@ -66,10 +67,42 @@ __global__ void __launch_bounds__(256) decode_stream_kernel(const DecodeArgs a) 
     extern __shared__ __align__(16) unsigned char smem[];
 
     const Problem &p = a.p;
-    const int kvh = blockIdx.x, c = blockIdx.y, seq = blockIdx.z;
+    const int C = a.C;
+    // Work item blockIdx.x -> (sequence, chunk, kv head), enumerating only the chunks that hold keys (kv head
+    // fastest): the workgroups with work come first in launch order and the dispatcher spreads them over all CUs;
+    // the tail of the upper-bound grid exits at once.
+    int seq, c;
+    {
+        const int lane_ = threadIdx.x & 63, cmax = p.max_pos / C;
+        int rest = (int)blockIdx.x / p.NKV;
+        seq = -1; c = 0;
+        for (int s0 = 0; s0 < p.nseq; s0 += 64) {
+            int n = 0, first = 0;
+            if (s0 + lane_ < p.nseq) {
+                const int ps = tok_pos(p, s0 + lane_, 0);
+                first = win_lo(ps, p.window) / C;
+                n = max(0, min(ps / C, cmax) - first + 1);
+            }
+            int incl = n;                                      // inclusive prefix sum over the 64 lanes
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(incl, o);
+                if (lane_ >= o) incl += y;
+            }
+            const unsigned long long hit = __ballot(incl > rest);
+            if (hit) {
+                const int l = __builtin_ctzll(hit);
+                seq = s0 + l;
+                c = __shfl(first, l) + rest - (__shfl(incl, l) - __shfl(n, l));
+                break;
+            }
+            rest -= __shfl(incl, 63);
+        }
+        if (seq < 0) return;
+    }
+    const int kvh = (int)blockIdx.x % p.NKV;
     const int GRP = p.NQ / p.NKV;
     const int pos = tok_pos(p, seq, 0), lo = win_lo(pos, p.window), hi = pos + 1;
-    const int C = a.C;
     const int j_lo = max(c * C, lo), j_hi = min(c * C + C, hi);
     if (j_lo >= j_hi) return;
 
@@ -80,14 +113,44 @@ __global__ void __launch_bounds__(256) decode_stream_kernel(const DecodeArgs a) 
     uint16_t *qs = reinterpret_cast<uint16_t *>(smem);
     float *redm = reinterpret_cast<float *>(smem + Cf::LDS_Q), *redl = redm + NW * 16, *buf = redl + NW * 16;
     uint16_t *vs = reinterpret_cast<uint16_t *>(smem + Cf::LDS_Q) + (size_t)wave * KT * Cf::VSTR;   // reused by the merge
+    uint16_t *kls = vs;                        // the K tile is consumed before the V tile lands in the same slice
 
-    for (int i = tid; i < 16 * (HD / 8); i += NW * 64) {
-        const int row = i / (HD / 8), col = (i % (HD / 8)) * 8;
-        u32x4 v = u32x4{0u, 0u, 0u, 0u};
-        if (row < GRP)
-            v = load8_op<QT, F16>(reinterpret_cast<const QE *>(p.Q) + ((size_t)seq * p.NQ + kvh * GRP + row) * HD + col);
-        *reinterpret_cast<u32x4 *>(qs + row * Cf::QSTR + col) = v;
+    // Q rows of the group (zero rows past GRP), requested first: the LDS store below then waits only for them.
+    constexpr int QCH = 16 * (HD / 8) / (NW * 64);
+    auto qrow_of = [&](int u) { return (tid + NW * 64 * u) / (HD / 8); };
+    auto qcol_of = [&](int u) { return ((tid + NW * 64 * u) % (HD / 8)) * 8; };
+    u32x4 qv[QCH];
+#pragma unroll
+    for (int u = 0; u < QCH; u++) {
+        qv[u] = u32x4{0u, 0u, 0u, 0u};
+        if (qrow_of(u) < GRP)
+            qv[u] = load8_op<QT, F16>(reinterpret_cast<const QE *>(p.Q) + ((size_t)seq * p.NQ + kvh * GRP + qrow_of(u)) * HD + qcol_of(u));
     }
+    // This wave's tiles: k = k0 .. k1-1 with tile k at key c*C + KT*(wave + NW*k), the ones meeting [j_lo, j_hi).
+    const int tb0 = j_lo / KT - c * (C / KT), tb1 = (j_hi - 1) / KT - c * (C / KT);   // tile range in the chunk
+    const int k0 = tb0 <= wave ? 0 : (tb0 - wave + NW - 1) / NW;
+    const int k1 = tb1 < wave ? 0 : (tb1 - wave) / NW + 1;
+    // Keys of a tile are attended without per-key tests when the tile lies inside [j_lo, j_hi) and below the tree.
+    const int full_hi = min(j_hi, p.anc ? pos : INT_MAX);
+    // Loads of tile k (K straight into A fragments; V rows coalesced for the private LDS transpose).
+    auto load = [&](int k, u32x4 (&kf)[Cf::VCH], u32x4 (&vr)[Cf::VCH]) {
+        const int jt = c * C + KT * (wave + NW * k);
+#pragma unroll
+        for (int u = 0; u < Cf::VCH; u++) {      // whole rows, 16 bytes per lane; the last tile clamps to the last key
+            const int q = lane + 64 * u, key = q / (HD / 8), col = (q % (HD / 8)) * 8;
+            const size_t off = (size_t)min(jt + key, hi - 1) * krow + col;
+            kf[u] = load8_op_stream<KVT, F16>(Kb + off);
+            vr[u] = load8_op_stream<KVT, F16>(Vb + off);
+        }
+    };
+    // PF + 1 register buffers: the loads of tiles k + 1 .. k + PF are in flight while tile k is computed (PF = 0:
+    // load, then compute; measured fastest on the B=16 ragged workload, where the lower register count lets every
+    // chunk's workgroup be resident at once). The first PF tiles are requested before the Q rows are staged.
+    constexpr int PF = 0, NBUF = PF + 1;
+    u32x4 kb[NBUF][Cf::VCH], vb[NBUF][Cf::VCH];
+    static_for<PF>([&](auto i) { if (k0 + i < k1) load(k0 + i, kb[i], vb[i]); });
+#pragma unroll
+    for (int u = 0; u < QCH; u++) *reinterpret_cast<u32x4 *>(qs + qrow_of(u) * Cf::QSTR + qcol_of(u)) = qv[u];
     RowMask rm;
     rm.pos = pos; rm.lo = lo; rm.valid = ln < GRP; rm.tree = p.anc != nullptr;
     rm.anc = p.anc ? p.anc[seq] : 0u; rm.tb = pos;
@@ -98,45 +161,26 @@ __global__ void __launch_bounds__(256) decode_stream_kernel(const DecodeArgs a) 
 #pragma unroll
     for (int db = 0; db < Cf::DB; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     const uint16_t *qrow = qs + ln * Cf::QSTR + 8 * g;
-    // This wave's tiles: k = k0 .. k1-1 with tile k at key c*C + KT*(wave + NW*k), the ones meeting [j_lo, j_hi).
-    const int tb0 = j_lo / KT - c * (C / KT), tb1 = (j_hi - 1) / KT - c * (C / KT);   // tile range in the chunk
-    const int k0 = tb0 <= wave ? 0 : (tb0 - wave + NW - 1) / NW;
-    const int k1 = tb1 < wave ? 0 : (tb1 - wave) / NW + 1;
-    // Keys of a tile are attended without per-key tests when the tile lies inside [j_lo, j_hi) and below the tree.
-    const int full_hi = min(j_hi, p.anc ? pos : INT_MAX);
-    const KE *kp = Kb + (size_t)(c * C + KT * (wave + NW * k0) + ln) * krow + 8 * g;
-    const KE *vp = Vb + (size_t)(c * C + KT * (wave + NW * k0) + ln) * krow + 8 * g;
-    const size_t kstep = (size_t)KT * NW * krow;
-#ifdef DGX_TRACE
-    const int tslot = (blockIdx.z == 3 && blockIdx.x == 1 && blockIdx.y < 16) ? (int)blockIdx.y * 4 + wave : -1;
-#define PT(ph) if (tslot >= 0 && lane == 0 && k - k0 < 16) g_ptrace[tslot][k - k0][ph] = __builtin_amdgcn_s_memtime();
-#else
-#define PT(ph)
-#endif
-    for (int k = k0; k < k1; k++, kp += kstep, vp += kstep) {
+    auto compute = [&](int k, const u32x4 (&kr)[Cf::VCH], const u32x4 (&vr)[Cf::VCH]) {
         const int jt = c * C + KT * (wave + NW * k);
-        PT(0)
-        const KE *kq = kp;
-        if (jt + KT > hi) kq = Kb + (size_t)min(jt + ln, hi - 1) * krow + 8 * g;   // last tile: clamp to the last key
-        u32x4 kf[Cf::KS], vr[Cf::VCH];
-#pragma unroll
-        for (int ks = 0; ks < Cf::KS; ks++) kf[ks] = load8_op<KVT, F16>(kq + 32 * ks);
-        // V tile rows, coalesced (HD/8 lanes per key row), for the private LDS transpose.
+        // K rows through the wave's LDS slice into MFMA A fragments (lane = key ln, 16 bytes of dims 32 ks + 8 g).
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int u = 0; u < Cf::VCH; u++) {
             const int q = lane + 64 * u, key = q / (HD / 8), col = (q % (HD / 8)) * 8;
-            vr[u] = load8_op<KVT, F16>(Vb + (size_t)min(jt + key, hi - 1) * krow + col);
+            *reinterpret_cast<u32x4 *>(kls + key * Cf::VSTR + col) = kr[u];
         }
+        __builtin_amdgcn_wave_barrier();
         // S^T[key jt + 4g + i][row ln], two independent MFMA chains.
         f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
 #pragma unroll
         for (int ks = 0; ks < Cf::KS; ks++) {
             const u32x4 qf = *reinterpret_cast<const u32x4 *>(qrow + 32 * ks);
-            if (ks & 1) s1 = mfma16<F16>(kf[ks], qf, s1);
-            else s0 = mfma16<F16>(kf[ks], qf, s0);
+            const u32x4 kf = *reinterpret_cast<const u32x4 *>(kls + ln * Cf::VSTR + 32 * ks + 8 * g);
+            if (ks & 1) s1 = mfma16<F16>(kf, qf, s1);
+            else s0 = mfma16<F16>(kf, qf, s0);
         }
         const f32x4 s = (s0 + s1) * a.sl2;
-        PT(1)
         // Online softmax (log2 domain), lazily moved reference max; l is this lane's share of the row sum.
         float tv[4];
         if (jt >= j_lo && jt + KT <= full_hi) {
@@ -165,8 +209,8 @@ __global__ void __launch_bounds__(256) decode_stream_kernel(const DecodeArgs a) 
         if (m == kNegInf) pv[0] = pv[1] = pv[2] = pv[3] = 0.f;
         l += (pv[0] + pv[1]) + (pv[2] + pv[3]);
         const u32x2 pop = u32x2{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3])};
-        PT(2)
         // O^T += V^T P^T (16x16x16): stage the V tile in this wave's LDS slice, read it back transposed.
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int u = 0; u < Cf::VCH; u++) {
             const int q = lane + 64 * u, key = q / (HD / 8), col = (q % (HD / 8)) * 8;
@@ -176,10 +220,15 @@ __global__ void __launch_bounds__(256) decode_stream_kernel(const DecodeArgs a) 
         const uint16_t *vt = vs + (4 * g + (ln >> 2)) * Cf::VSTR + 4 * (ln & 3);
 #pragma unroll
         for (int db = 0; db < Cf::DB; db++) acc[db] = mfma16k16<F16>(lds_read_tr16(vt + 16 * db), pop, acc[db]);
-        __builtin_amdgcn_wave_barrier();
-        PT(3)
+    };
+    for (int k = k0; k < k1; k += NBUF) {
+        static_for<NBUF>([&](auto j) {
+            const int kk = k + j;
+            if (kk >= k1) return;
+            if (kk + PF < k1) load(kk + PF, kb[(j + PF) % NBUF], vb[(j + PF) % NBUF]);
+            compute(kk, kb[j], vb[j]);
+        });
     }
-#undef PT
     l = sum_over_groups(l);
 #ifdef DGX_TRACE
     if (lane == 0) {
@@ -190,7 +239,7 @@ __global__ void __launch_bounds__(256) decode_stream_kernel(const DecodeArgs a) 
         g_dtrace[bid & 0xffff][0] = t_start;
         g_dtrace[bid & 0xffff][1] = __builtin_amdgcn_s_memrealtime();
         g_dtrace[bid & 0xffff][2] = (j_hi - j_lo + 15) / 16;
-        g_dtrace[bid & 0xffff][3] = (xcc & 0xf) | (((hwid >> 8) & 0xf) << 4) | (((hwid >> 12) & 0x7) << 8) | (((hwid >> 4) & 3) << 12);
+        g_dtrace[bid & 0xffff][3] = (unsigned long long)(xcc & 0xf) | ((unsigned long long)hwid << 4);
     }
 #endif
 
@@ -235,16 +284,21 @@ __global__ void __launch_bounds__(256) decode_stream_kernel(const DecodeArgs a) 
 }
 
 template <int HD, int KVT, int QT>
-static hipError_t launch_dec_t(const DecodeArgs &a, dim3 grid, hipStream_t st) {
-    hipLaunchKernelGGL((decode_stream_kernel<HD, KVT, QT>), grid, dim3(256), DecodeCfg<HD>::LDS, st, a);
+static hipError_t launch_dec_t(const DecodeArgs &a, dim3 grid, int nw, hipStream_t st) {
+    switch (nw) {
+    case 1: hipLaunchKernelGGL((decode_stream_kernel<HD, 1, KVT, QT>), grid, dim3(64), (DecodeCfg<HD, 1>::LDS), st, a); break;
+    case 2: hipLaunchKernelGGL((decode_stream_kernel<HD, 2, KVT, QT>), grid, dim3(128), (DecodeCfg<HD, 2>::LDS), st, a); break;
+    case 4: hipLaunchKernelGGL((decode_stream_kernel<HD, 4, KVT, QT>), grid, dim3(256), (DecodeCfg<HD, 4>::LDS), st, a); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
 template <int KVT, int QT>
-static hipError_t dec_dispatch_hd(const DecodeArgs &a, dim3 grid, hipStream_t st) {
+static hipError_t dec_dispatch_hd(const DecodeArgs &a, dim3 grid, int nw, hipStream_t st) {
     switch (a.p.HD) {
-    case 128: return launch_dec_t<128, KVT, QT>(a, grid, st);
-    case 256: return launch_dec_t<256, KVT, QT>(a, grid, st);
+    case 128: return launch_dec_t<128, KVT, QT>(a, grid, nw, st);
+    case 256: return launch_dec_t<256, KVT, QT>(a, grid, nw, st);
     default: return hipErrorNotSupported;
     }
 }
@@ -259,13 +313,15 @@ hipError_t launch_decode_stream(const Problem &p, int chunk, const Partials &par
     if (chunk <= 0 || chunk % 16) return hipErrorInvalidValue;
     if (p.max_pos / chunk + 1 > part.ns_cap) return hipErrorInvalidValue;
     DecodeArgs a{p, part, chunk, p.scale * kLog2e};
-    dim3 grid(p.NKV, p.max_pos / chunk + 1, p.nseq);
-    if (grid.z > 65535u || grid.y > 65535u) return hipErrorInvalidConfiguration;
+    const long long items = (long long)p.NKV * (p.max_pos / chunk + 1) * p.nseq;   // upper bound of the work items
+    if (items > INT_MAX) return hipErrorInvalidConfiguration;
+    dim3 grid((unsigned)items);
+    const int nw = 2;   // two waves per chunk: every chunk of the B=16 ragged batch is resident at once
     const int kv = p.kv_dtype, q = p.q_dtype;
-    if (kv == DT_F16 && q == DT_FP32) return dec_dispatch_hd<DT_F16, DT_FP32>(a, grid, st);
-    if (kv == DT_F16 && q == DT_F16) return dec_dispatch_hd<DT_F16, DT_F16>(a, grid, st);
-    if (kv == DT_BF16 && q == DT_FP32) return dec_dispatch_hd<DT_BF16, DT_FP32>(a, grid, st);
-    if (kv == DT_BF16 && q == DT_BF16) return dec_dispatch_hd<DT_BF16, DT_BF16>(a, grid, st);
+    if (kv == DT_F16 && q == DT_FP32) return dec_dispatch_hd<DT_F16, DT_FP32>(a, grid, nw, st);
+    if (kv == DT_F16 && q == DT_F16) return dec_dispatch_hd<DT_F16, DT_F16>(a, grid, nw, st);
+    if (kv == DT_BF16 && q == DT_FP32) return dec_dispatch_hd<DT_BF16, DT_FP32>(a, grid, nw, st);
+    if (kv == DT_BF16 && q == DT_BF16) return dec_dispatch_hd<DT_BF16, DT_BF16>(a, grid, nw, st);
     return hipErrorNotSupported;
 }
 

@@ -11,8 +11,15 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 
 namespace dgx {
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>): compile-time indices into register arrays.
+template <int I, int N, class F> __device__ __forceinline__ void static_for_(F &&f) {
+    if constexpr (I < N) { f(std::integral_constant<int, I>{}); static_for_<I + 1, N>(f); }
+}
+template <int N, class F> __device__ __forceinline__ void static_for(F &&f) { static_for_<0, N>(f); }
 
 enum DType : int { DT_FP32 = 0, DT_F16 = 1, DT_BF16 = 2 };   // same codes as KV_FP32/KV_F16/KV_BF16
 
@@ -69,6 +76,32 @@ __device__ __forceinline__ u32x4 load8_op(const typename Elem<DT>::T *p) {
         return *reinterpret_cast<const u32x4 *>(p);                       // same 16-bit format: raw bits
     } else {
         const u32x4 raw = *reinterpret_cast<const u32x4 *>(p);            // the other 16-bit format: convert
+        u32x4 r;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t w = raw[i];
+            const float lo = elem_to_f32<DT>((uint16_t)(w & 0xffffu)), hi = elem_to_f32<DT>((uint16_t)(w >> 16));
+            r[i] = pack2<F16>(lo, hi);
+        }
+        return r;
+    }
+}
+
+// The same from a streamed-once source (K/V in decode): non-temporal loads, which keep the caches for data that is
+// reused and sustain a higher HBM read rate.
+template <int DT, bool F16>
+__device__ __forceinline__ u32x4 load8_op_stream(const typename Elem<DT>::T *p) {
+    if constexpr (DT == DT_FP32) {
+        const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+        const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p) + 1);
+        u32x4 r;
+        r.x = pack2<F16>(a.x, a.y); r.y = pack2<F16>(a.z, a.w);
+        r.z = pack2<F16>(b.x, b.y); r.w = pack2<F16>(b.z, b.w);
+        return r;
+    } else if constexpr ((DT == DT_F16) == F16) {
+        return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    } else {
+        const u32x4 raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
         u32x4 r;
 #pragma unroll
         for (int i = 0; i < 4; i++) {

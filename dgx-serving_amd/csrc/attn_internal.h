@@ -46,10 +46,7 @@ __device__ __forceinline__ int win_lo(int pos, int window) {
 }
 
 // Split-KV decode / verify / tree kernel (waves split the keys of a chunk, small query-row tiles).
-// counters: zero-initialised ints, one per (sequence, token tile, kv head) (split_counter_count); when given,
-// the kernel also performs the LSE combine (the last workgroup of each group merges) and leaves them zero.
-hipError_t launch_split(const Problem &p, int chunk, const Partials &part, int *counters, hipStream_t st);
-size_t split_counter_count(const Problem &p);
+hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipStream_t st);
 // Streaming decode kernel for one query token per sequence (T == 1, HD 128/256, GRP <= 16, 16-bit cache);
 // hipErrorNotSupported for other shapes. Writes chunk partials for launch_combine.
 bool decode_stream_supported(const Problem &p);

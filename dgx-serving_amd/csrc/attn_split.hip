@@ -36,20 +36,7 @@ struct SplitArgs {
     int tpb;        // query tokens per workgroup
     int nchunks;    // token tiles per sequence
     float sl2;      // scale * log2(e)
-    int *counters;  // per (sequence, token tile, kv head) arrival counters for the fused combine, or null
 };
-
-// LSE combine of one (row, head) for 4 consecutive output dims d4*4..+3, over the row's valid chunks
-// [lo/C, pos/C] in ascending order (attention_decode_split.cuh:147-165): O = sum w_c acc_c / sum w_c l_c with
-// w_c = 2^(m_c - max m). Shared by the fused epilogue and the stand-alone combine kernel, so both produce the
-// same bits.
-// Agent-scope relaxed atomic accesses of the partials: they are written through to the device coherence point
-// and read from it, so workgroups on different XCDs exchange partials without an L2 write-back or invalidate.
-__device__ __forceinline__ void st_agent(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ float ld_agent(const float *p) {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_part(const float *p, bool agent) { return agent ? ld_agent(p) : *p; }
 
 // Wave-wide reductions over all 64 lanes (fixed xor-butterfly order, identical result in every lane).
 __device__ __forceinline__ float wave_max(float v) {
@@ -61,82 +48,100 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// LSE combine of one (row, head) by one wave, over the row's valid chunks [lo/C, pos/C]
-// (attention_decode_split.cuh:147-165): O = sum_c w_c acc_c / sum_c w_c l_c with w_c = 2^(m_c - max m).
-// Lanes load the chunk statistics in parallel (64 chunks per round), the weights are broadcast from lanes,
-// and each lane accumulates 4 head dims over the chunks in ascending order with 8 loads in flight.
-// Shared by the fused epilogue and the stand-alone combine kernel, so both give the same bits.
+// LSE combine of the chunk partials of one (row, head) by one wave. Lane c holds the statistics of chunk c (64
+// at a time); lane d holds 4 head dims. The partial accumulators of the first NB chunks are requested before
+// the statistics are reduced, so a row with up to NB chunks costs one memory round trip. Chunks are summed in
+// increasing order, each weighted by 2^(m_c - max m) (a fixed order: the result depends only on the row).
 template <int HD>
-__device__ __forceinline__ void combine_wave(const Problem &p, const Partials &part, int C, int s, int t, int h,
-                                             bool agent) {
+__device__ __forceinline__ void combine_wave(const Problem &p, const Partials &part, int C, int s, int t, int h) {
+    constexpr int D4 = HD / 4;                       // 4-dim groups of a row
+    constexpr int NP = (D4 + 63) / 64;               // passes of 64 lanes over the row
+    constexpr int NB = HD >= 512 ? 16 : 32;          // partial rows in flight per lane
     const int lane = threadIdx.x & 63;
     const int r = s * p.T + t;
     const int pos = tok_pos(p, s, t), lo = win_lo(pos, p.window);
     const int c_lo = lo / C, n = pos / C - c_lo + 1;
     const size_t base = ((size_t)r * p.NQ + h) * part.ns_cap + c_lo;
-    float mg = kNegInf;
-    for (int c0 = 0; c0 < n; c0 += 64)
-        if (c0 + lane < n) mg = fmaxf(mg, ld_part(part.m + base + c0 + lane, agent));
+    const float *accb = part.acc + base * HD;
+    f32x4 v[NB];
+    auto load_batch = [&](int c0, int d4) {
+#pragma unroll
+        for (int u = 0; u < NB; u++) v[u] = *reinterpret_cast<const f32x4 *>(accb + (size_t)min(c0 + u, n - 1) * HD + 4 * d4);
+    };
+    load_batch(0, min(lane, D4 - 1));                // in flight while the statistics are reduced
+    const float m0 = lane < n ? part.m[base + lane] : kNegInf;
+    const float l0 = lane < n ? part.l[base + lane] : 0.f;
+    float mg = m0;
+    for (int c0 = 64; c0 < n; c0 += 64)
+        if (c0 + lane < n) mg = fmaxf(mg, part.m[base + c0 + lane]);
     mg = wave_max(mg);
-    float L = 0.f;
-    for (int c0 = 0; c0 < n; c0 += 64) {
+    float L = wave_sum((m0 != kNegInf && mg != kNegInf) ? l0 * fast_exp2(m0 - mg) : 0.f);
+    for (int c0 = 64; c0 < n; c0 += 64) {
         float x = 0.f;
         if (c0 + lane < n && mg != kNegInf) {
-            const float mc = ld_part(part.m + base + c0 + lane, agent);
-            if (mc != kNegInf) x = ld_part(part.l + base + c0 + lane, agent) * fast_exp2(mc - mg);
+            const float mc = part.m[base + c0 + lane];
+            if (mc != kNegInf) x = part.l[base + c0 + lane] * fast_exp2(mc - mg);
         }
         L += wave_sum(x);
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    constexpr int D4 = HD / 4;                       // 4-dim groups of a row
-    for (int d4 = lane; d4 < D4; d4 += 64) {
+    const float w0 = (m0 != kNegInf && mg != kNegInf) ? fast_exp2(m0 - mg) : 0.f;
+#pragma unroll
+    for (int ps = 0; ps < NP; ps++) {
+        const int d4 = lane + 64 * ps;
         f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int c0 = 0; c0 < n; c0 += 64) {
-            float w = 0.f;
-            if (c0 + lane < n && mg != kNegInf) {
-                const float mc = ld_part(part.m + base + c0 + lane, agent);
-                if (mc != kNegInf) w = fast_exp2(mc - mg);
+        for (int c0 = 0; c0 < n; c0 += NB) {
+            if (ps > 0 || c0 > 0) load_batch(c0, min(d4, D4 - 1));
+            float w = w0;                            // weights of the 64-chunk group holding this batch
+            if (c0 >= 64) {
+                const int c = (c0 & ~63) + lane;
+                const float mc = c < n ? part.m[base + c] : kNegInf;
+                w = (mc != kNegInf && mg != kNegInf) ? fast_exp2(mc - mg) : 0.f;
             }
-            const int nn = min(64, n - c0);
-            for (int c = 0; c < nn; c += 8) {
-                f32x4 v[8];
-                float wc[8];
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    wc[u] = __shfl(w, min(c + u, nn - 1));
-                    const float *pa = part.acc + (base + c0 + min(c + u, nn - 1)) * HD + 4 * d4;
-                    if (agent) v[u] = f32x4{ld_agent(pa), ld_agent(pa + 1), ld_agent(pa + 2), ld_agent(pa + 3)};
-                    else v[u] = *reinterpret_cast<const f32x4 *>(pa);
-                }
-#pragma unroll
-                for (int u = 0; u < 8; u++)
-                    if (c + u < nn && wc[u] != 0.f) acc += v[u] * wc[u];
+            for (int u = 0; u < NB; u++) {
+                const float wc = __shfl(w, (c0 + u) & 63);
+                if (c0 + u < n && wc != 0.f) acc += v[u] * wc;
             }
         }
-        const f32x4 o = acc * inv;
-        const size_t oi = ((size_t)r * p.NQ + h) * HD + 4 * d4;
-        if (p.o_dtype == DT_FP32) *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.O) + oi) = o;
-        else {
-            const bool f16 = p.o_dtype == DT_F16;
-            const u32x2 ow = u32x2{(uint32_t)f32_to_op(o.x, f16) | ((uint32_t)f32_to_op(o.y, f16) << 16),
-                                   (uint32_t)f32_to_op(o.z, f16) | ((uint32_t)f32_to_op(o.w, f16) << 16)};
-            *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(p.O) + oi) = ow;
+        if (d4 < D4) {
+            const f32x4 o = acc * inv;
+            const size_t oi = ((size_t)r * p.NQ + h) * HD + 4 * d4;
+            if (p.o_dtype == DT_FP32) *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.O) + oi) = o;
+            else {
+                const bool f16 = p.o_dtype == DT_F16;
+                const u32x2 ow = u32x2{(uint32_t)f32_to_op(o.x, f16) | ((uint32_t)f32_to_op(o.y, f16) << 16),
+                                       (uint32_t)f32_to_op(o.z, f16) | ((uint32_t)f32_to_op(o.w, f16) << 16)};
+                *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(p.O) + oi) = ow;
+            }
         }
     }
     if (p.lse && lane == 0) p.lse[(size_t)r * p.NQ + h] = (L > 0.f) ? (mg + log2f(L)) * kLn2 : kNegInf;
 }
 
+#ifndef DGX_SPLIT_STAGES
+#define DGX_SPLIT_STAGES 2
+#endif
+#ifndef DGX_SPLIT_NW
+#define DGX_SPLIT_NW 4
+#endif
+#ifndef DGX_SPLIT_KT
+#define DGX_SPLIT_KT 16
+#endif
 template <int HD, int RB>
 struct SplitCfg {
-    static constexpr int NW = 4;              // waves per workgroup; wave w owns head dims [w*HD/4, (w+1)*HD/4)
-    static constexpr int KT = 16;             // keys per tile
+    static constexpr int NW = DGX_SPLIT_NW;   // waves per workgroup; wave w owns head dims [w*HD/NW, (w+1)*HD/NW)
+    static constexpr int KT = DGX_SPLIT_KT;   // keys per tile (KT/16 sub-tiles of 16 keys)
+    static constexpr int NSUB = KT / 16;
     static constexpr int KS = HD / 32;        // QK k-steps (16x16x32)
-    static constexpr int DBW = HD / 64;       // PV output dim blocks (16x16x16) per wave
+    static constexpr int DBW = HD / 16 / NW;  // PV output dim blocks (16x16x16) per wave
     static constexpr int STR = HD + 8;        // LDS row stride of Q, K and V tiles (16-bit elements)
     static constexpr int RR = RB * 16;        // query rows per workgroup
     static constexpr int CPT = KT * HD / 8 / (NW * 64);   // 16-byte chunks per thread per tile (K and V each)
+    static constexpr int NSTG = DGX_SPLIT_STAGES;        // register stages of the K/V stream
     static constexpr size_t TILE = (size_t)KT * STR;      // elements of one K or V tile
-    static constexpr size_t LDS = ((size_t)RR * STR + 4 * TILE) * 2;   // Q + (K, V) x double buffer
+    static constexpr bool QREG = RB * KS <= 8;            // Q fragments live in registers (straight from HBM)
+    static constexpr size_t LDS = ((QREG ? 0 : (size_t)RR * STR) + 4 * TILE) * 2;   // [Q] + (K, V) x double buffer
     static_assert(CPT >= 1 && (KT * HD / 8) % (NW * 64) == 0, "tile chunks");
 };
 
@@ -181,18 +186,33 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
     const size_t krow = (size_t)p.NKV * HD;
     const KE *Kb = reinterpret_cast<const KE *>(p.K) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
     const KE *Vb = reinterpret_cast<const KE *>(p.V) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
+    constexpr bool QREG = Cf::QREG;
     uint16_t *qs = reinterpret_cast<uint16_t *>(smem);
-    uint16_t *tiles = qs + (size_t)Cf::RR * Cf::STR;           // [buf][K | V][KT][STR]
+    uint16_t *tiles = qs + (QREG ? 0 : (size_t)Cf::RR * Cf::STR);   // [buf][K | V][KT][STR]
 
-    // Q rows of the workgroup -> LDS in the MFMA operand format (row rho = token-major (token, head)).
-    for (int i = tid; i < Cf::RR * (HD / 8); i += NW * 64) {
-        const int rho = i / (HD / 8), col = (i % (HD / 8)) * 8;
-        u32x4 v = u32x4{0u, 0u, 0u, 0u};
-        if (rho < nrows) {
-            const int t = tok0 + rho / GRP, h = kvh * GRP + rho % GRP;
-            v = load8_op<QT, F16>(reinterpret_cast<const QE *>(p.Q) + ((size_t)(seq * p.T + t) * p.NQ + h) * HD + col);
+    // Q rows of the workgroup (row rho = token-major (token, head)) in the MFMA operand format: straight into
+    // registers when they fit (lane (row ln, group g) holds dims 32 ks + 8 g ..), else through LDS.
+    u32x4 qreg[QREG ? RB : 1][QREG ? Cf::KS : 1];
+    if constexpr (QREG) {
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            const int rho = rb * 16 + ln;
+            const bool ok = rho < nrows;
+            const int t = tok0 + (ok ? rho / GRP : 0), h = kvh * GRP + (ok ? rho % GRP : 0);
+            const QE *qrow = reinterpret_cast<const QE *>(p.Q) + ((size_t)(seq * p.T + t) * p.NQ + h) * HD + 8 * g;
+#pragma unroll
+            for (int ks = 0; ks < Cf::KS; ks++) qreg[rb][ks] = ok ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
         }
-        *reinterpret_cast<u32x4 *>(qs + rho * Cf::STR + col) = v;
+    } else {
+        for (int i = tid; i < Cf::RR * (HD / 8); i += NW * 64) {
+            const int rho = i / (HD / 8), col = (i % (HD / 8)) * 8;
+            u32x4 v = u32x4{0u, 0u, 0u, 0u};
+            if (rho < nrows) {
+                const int t = tok0 + rho / GRP, h = kvh * GRP + rho % GRP;
+                v = load8_op<QT, F16>(reinterpret_cast<const QE *>(p.Q) + ((size_t)(seq * p.T + t) * p.NQ + h) * HD + col);
+            }
+            *reinterpret_cast<u32x4 *>(qs + rho * Cf::STR + col) = v;
+        }
     }
     RowMask rm[RB];
 #pragma unroll
@@ -217,8 +237,10 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
     if (p.anc) pos_min = min(pos_min, tok_pos(p, seq, 0) - 1);   // tree keys are never in the fast path
 
     // Cooperative tile fetch (global -> registers): chunk q = tid + 256*u -> key q / (HD/8), column (q % (HD/8))*8.
-    // Two register stages keep the loads of tile it+2 in flight while tile it is computed from LDS.
-    u32x4 kr0[Cf::CPT], vr0[Cf::CPT], kr1[Cf::CPT], vr1[Cf::CPT];
+    // NSTG register stages keep the loads of the next NSTG tiles in flight while tile it is computed from LDS (HBM
+    // bandwidth grows with the bytes in flight, and a decode tile's compute is short).
+    constexpr int NSTG = Cf::NSTG;
+    u32x4 kst[NSTG][Cf::CPT], vst[NSTG][Cf::CPT];
     auto fetch = [&](u32x4 (&kr)[Cf::CPT], u32x4 (&vr)[Cf::CPT], int jt) {
 #pragma unroll
         for (int u = 0; u < Cf::CPT; u++) {
@@ -248,55 +270,55 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
     }
     const int jb = (j_lo / Cf::KT) * Cf::KT;
     const int ntile = (j_hi - jb + Cf::KT - 1) / Cf::KT;
-    fetch(kr0, vr0, jb);
-    fetch(kr1, vr1, jb + Cf::KT);
-    stash(kr0, vr0, 0);
-    __syncthreads();                                           // Q rows and tile 0 are in LDS
-    constexpr bool QREG = RB * Cf::KS <= 8;                    // Q fragments in registers when they fit
-    u32x4 qreg[QREG ? RB : 1][QREG ? Cf::KS : 1];
-    if constexpr (QREG) {
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++)
-#pragma unroll
-            for (int ks = 0; ks < Cf::KS; ks++)
-                qreg[rb][ks] = *reinterpret_cast<const u32x4 *>(qs + (rb * 16 + ln) * Cf::STR + 32 * ks + 8 * g);
-    }
+    for (int k = 0; k < NSTG; k++) fetch(kst[k], vst[k], jb + Cf::KT * k);
+    stash(kst[0], vst[0], 0);
+    __syncthreads();                                           // tile 0 (and the Q rows without QREG) in LDS
 
     auto compute = [&](int it) {
         const int jt = jb + Cf::KT * it;
         const uint16_t *kt = tiles + (size_t)(it & 1) * 2 * Cf::TILE, *vt = kt + Cf::TILE;
-        // S^T[key][row] = K Q^T (every wave computes the whole tile) as two independent MFMA chains.
-        f32x4 s[RB], s2[RB];
+        // S^T[key][row] = K Q^T (every wave computes the whole tile), two independent MFMA chains per sub-tile.
+        constexpr int NSUB = Cf::NSUB;
+        f32x4 s[NSUB][RB], s2[NSUB][RB];
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++) s[rb] = s2[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int sub = 0; sub < NSUB; sub++)
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) s[sub][rb] = s2[sub][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < Cf::KS; ks++) {
-            const u32x4 kf = *reinterpret_cast<const u32x4 *>(kt + ln * Cf::STR + 32 * ks + 8 * g);
 #pragma unroll
-            for (int rb = 0; rb < RB; rb++) {
-                u32x4 qf;
-                if constexpr (QREG) qf = qreg[rb][ks];
-                else qf = *reinterpret_cast<const u32x4 *>(qs + (rb * 16 + ln) * Cf::STR + 32 * ks + 8 * g);
-                if (ks & 1) s2[rb] = mfma16<F16>(kf, qf, s2[rb]);
-                else s[rb] = mfma16<F16>(kf, qf, s[rb]);
+            for (int sub = 0; sub < NSUB; sub++) {
+                const u32x4 kf = *reinterpret_cast<const u32x4 *>(kt + (16 * sub + ln) * Cf::STR + 32 * ks + 8 * g);
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) {
+                    u32x4 qf;
+                    if constexpr (QREG) qf = qreg[rb][ks];
+                    else qf = *reinterpret_cast<const u32x4 *>(qs + (rb * 16 + ln) * Cf::STR + 32 * ks + 8 * g);
+                    if (ks & 1) s2[sub][rb] = mfma16<F16>(kf, qf, s2[sub][rb]);
+                    else s[sub][rb] = mfma16<F16>(kf, qf, s[sub][rb]);
+                }
             }
         }
-#pragma unroll
-        for (int rb = 0; rb < RB; rb++) s[rb] += s2[rb];
-        // Online softmax (log2 domain) with a lazily moved reference max m (see kRescaleThreshold). l holds
-        // this lane's share of the row sum; the four lanes of a row are added once, after the loop.
+        // Online softmax (log2 domain) over the tile's keys with a lazily moved reference max m (see
+        // kRescaleThreshold). l holds this lane's share of the row sum; the four lanes of a row are added once,
+        // after the loop.
         const bool full = jt >= j_lo && jt + Cf::KT <= j_hi && jt >= lo_max && jt + Cf::KT - 1 <= pos_min;
-        u32x2 pop[RB];
-        float tv[RB][4];
+        u32x2 pop[NSUB][RB];
+        float tv[NSUB][RB][4];
         bool need = false;
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
             float mx = kNegInf;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int key = jt + 4 * g + i;
-                const float v = (full || (key >= j_lo && key < j_hi && rm[rb].attends(key))) ? s[rb][i] * a.sl2 : kNegInf;
-                tv[rb][i] = v; mx = fmaxf(mx, v);
+            for (int sub = 0; sub < NSUB; sub++) {
+                const f32x4 sc = s[sub][rb] + s2[sub][rb];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int key = jt + 16 * sub + 4 * g + i;
+                    const float v = (full || (key >= j_lo && key < j_hi && rm[rb].attends(key))) ? sc[i] * a.sl2 : kNegInf;
+                    tv[sub][rb][i] = v; mx = fmaxf(mx, v);
+                }
             }
             mx = max_over_groups(mx);
             if (mx > m[rb] + kRescaleThreshold) { mnew[rb] = mx; need = true; } else mnew[rb] = m[rb];
@@ -311,38 +333,49 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
             }
         }
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++) {
-            float pv[4];
+        for (int sub = 0; sub < NSUB; sub++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) { pv[i] = (tv[rb][i] == kNegInf) ? 0.f : fast_exp2(tv[rb][i] - m[rb]); l[rb] += pv[i]; }
-            pop[rb] = u32x2{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3])};
-        }
+            for (int rb = 0; rb < RB; rb++) {
+                float pv[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) { pv[i] = (tv[sub][rb][i] == kNegInf) ? 0.f : fast_exp2(tv[sub][rb][i] - m[rb]); l[rb] += pv[i]; }
+                pop[sub][rb] = u32x2{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3])};
+            }
         // O^T[this wave's dims] += V^T P^T (16x16x16): the A fragment is a transposed LDS read of the V tile.
-        const uint16_t *vtr = vt + (4 * g + (ln >> 2)) * Cf::STR + wave * (HD / NW) + 4 * (ln & 3);
 #pragma unroll
-        for (int db = 0; db < Cf::DBW; db++) {
-            const u32x2 vop = lds_read_tr16(vtr + 16 * db);
+        for (int sub = 0; sub < NSUB; sub++) {
+            const uint16_t *vtr = vt + (16 * sub + 4 * g + (ln >> 2)) * Cf::STR + wave * (HD / NW) + 4 * (ln & 3);
 #pragma unroll
-            for (int rb = 0; rb < RB; rb++) acc[rb][db] = mfma16k16<F16>(vop, pop[rb], acc[rb][db]);
+            for (int db = 0; db < Cf::DBW; db++) {
+                const u32x2 vop = lds_read_tr16(vtr + 16 * db);
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) acc[rb][db] = mfma16k16<F16>(vop, pop[sub][rb], acc[rb][db]);
+            }
         }
     };
-    // Iteration it: fetch tile it+2 into the register stage that held tile it, compute tile it from LDS, stash
-    // tile it+1 (fetched one iteration earlier) into the other LDS buffer, barrier. Fetches and stashes are
-    // unconditional (past the last tile a fetch re-reads the last key row, an L2 hit, and a stash fills a buffer
-    // that is never read again) so that every wait before a stash sees exactly the newer tile's loads in flight
-    // and the compiler never has to drain the pipeline at a control-flow merge.
+    // Step it (stage k = it % NSTG): refill stage k with tile it+NSTG, compute tile it from LDS, stash tile it+1
+    // (stage (k+1) % NSTG) into the other LDS buffer, barrier. Fetches and stashes are unconditional (past the last
+    // tile a fetch re-reads the last key row, an L2 hit, and a stash fills a buffer that is never read again) so
+    // that every wait before a stash sees exactly the younger stages' loads in flight and the compiler never has
+    // to drain the pipeline at a control-flow merge.
     int it = 0;
-    for (; it + 1 < ntile; it += 2) {
-        fetch(kr0, vr0, jb + Cf::KT * (it + 2));
-        compute(it);
-        stash(kr1, vr1, 1);
-        __syncthreads();
-        fetch(kr1, vr1, jb + Cf::KT * (it + 3));
-        compute(it + 1);
-        stash(kr0, vr0, 0);
-        __syncthreads();
+    for (; it + NSTG <= ntile; it += NSTG) {
+#pragma unroll
+        for (int k = 0; k < NSTG; k++) {
+            fetch(kst[k], vst[k], jb + Cf::KT * (it + k + NSTG));
+            compute(it + k);
+            stash(kst[(k + 1) % NSTG], vst[(k + 1) % NSTG], (it + k + 1) & 1);
+            __syncthreads();
+        }
     }
-    if (it < ntile) compute(it);                                // odd tile count: the last tile sits in buffer 0
+#pragma unroll
+    for (int k = 0; k < NSTG; k++) {                            // the last ntile % NSTG tiles
+        if (it + k < ntile) {
+            compute(it + k);
+            stash(kst[(k + 1) % NSTG], vst[(k + 1) % NSTG], (it + k + 1) & 1);
+            __syncthreads();
+        }
+    }
 #ifdef DGX_TRACE
     if (tid == 0) {
         const size_t bid = ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
@@ -371,46 +404,21 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
 #pragma unroll
         for (int db = 0; db < Cf::DBW; db++) {
             float *dst = a.part.acc + pi * HD + wave * (HD / NW) + 16 * db + 4 * g;
-            const f32x4 v = acc[rb][db];
-            if (a.counters) { st_agent(dst, v.x); st_agent(dst + 1, v.y); st_agent(dst + 2, v.z); st_agent(dst + 3, v.w); }
-            else *reinterpret_cast<f32x4 *>(dst) = v;
+            *reinterpret_cast<f32x4 *>(dst) = acc[rb][db];
         }
         if (wave == 0 && g == 0) {
-            if (a.counters) { st_agent(a.part.m + pi, m[rb]); st_agent(a.part.l + pi, l[rb]); }
-            else { a.part.m[pi] = m[rb]; a.part.l[pi] = l[rb]; }
+            a.part.m[pi] = m[rb]; a.part.l[pi] = l[rb];
         }
     }
-    if (!a.counters) return;
-
-    // Fused combine: the last workgroup of this (sequence, token tile, kv head) to finish merges all chunk
-    // partials of its rows. Partials travel as agent-scope atomics (written through, read from the coherence
-    // point); each wave waits for its stores to complete before the barrier, so the counter increment that
-    // follows is ordered after every partial of the workgroup without any cache-wide write-back.
-    __shared__ int s_last;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    int *cnt = a.counters + ((size_t)seq * a.nchunks + tchunk) * p.NKV + kvh;
-    if (threadIdx.x == 0) {
-        // Chunks that exist in the grid and intersect the group's key range (a max_pos below the true positions
-        // drops keys, as in the reference, but keeps the counters consistent).
-        const int expected = min((hi_b - 1) / C, (int)gridDim.y - 1) - lo_b / C + 1;
-        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (old == expected - 1);
-        if (s_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    for (int row = wave; row < nrows; row += NW)
-        combine_wave<HD>(p, a.part, C, seq, tok0 + row / GRP, kvh * GRP + row % GRP, true);
 }
 
-// Stand-alone LSE combine: one wave per (row, head); used when no arrival counters are supplied.
+// LSE combine: one wave per (row, head).
 template <int HD>
 __global__ void __launch_bounds__(256) combine_kernel(const Problem p, const Partials part, int C) {
     const int rh = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (rh >= p.nseq * p.T * p.NQ) return;
     const int r = rh / p.NQ, h = rh % p.NQ;
-    combine_wave<HD>(p, part, C, r / p.T, r % p.T, h, false);
+    combine_wave<HD>(p, part, C, r / p.T, r % p.T, h);
 }
 
 // ---------------------------------------------------------------- host side
@@ -433,8 +441,10 @@ static hipError_t dispatch_rb(const SplitArgs &a, int RB, dim3 grid, hipStream_t
     switch (RB) {
     case 1: return launch_split_t<HD, 1, KVT, QT>(a, grid, st);
     case 2: return launch_split_t<HD, 2, KVT, QT>(a, grid, st);
+#ifndef DGX_SPLIT_EXPERIMENT
     case 3: return launch_split_t<HD, 3, KVT, QT>(a, grid, st);
     case 4: return launch_split_t<HD, 4, KVT, QT>(a, grid, st);
+#endif
     default: return hipErrorInvalidValue;
     }
 }
@@ -442,9 +452,11 @@ static hipError_t dispatch_rb(const SplitArgs &a, int RB, dim3 grid, hipStream_t
 template <int KVT, int QT>
 static hipError_t dispatch_hd(const SplitArgs &a, int RB, dim3 grid, hipStream_t st) {
     switch (a.p.HD) {
+#ifndef DGX_SPLIT_EXPERIMENT
     case 128: return dispatch_rb<128, KVT, QT>(a, RB, grid, st);
-    case 256: return dispatch_rb<256, KVT, QT>(a, RB, grid, st);
     case 512: return dispatch_rb<512, KVT, QT>(a, RB, grid, st);
+#endif
+    case 256: return dispatch_rb<256, KVT, QT>(a, RB, grid, st);
     default: return hipErrorInvalidValue;
     }
 }
@@ -461,21 +473,14 @@ static void split_tiling(const Problem &p, int &RB, int &tpb, int &nchunks) {
     nchunks = (p.T + tpb - 1) / tpb;
 }
 
-size_t split_counter_count(const Problem &p) {
-    int RB, tpb, nchunks;
-    split_tiling(p, RB, tpb, nchunks);
-    return (size_t)p.nseq * nchunks * p.NKV;
-}
-
 size_t partial_rows(const Problem &p, int chunk) {
     return (size_t)p.nseq * p.T * p.NQ * (size_t)(p.max_pos / chunk + 1);
 }
 
-hipError_t launch_split(const Problem &p, int chunk, const Partials &part, int *counters, hipStream_t st) {
+hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipStream_t st) {
     if (chunk <= 0 || chunk % 16) return hipErrorInvalidValue;
-    // Opt-in: the LDS-free streaming decode kernel (measured slower than the LDS-staged path on the B=16 ragged
-    // workload, kept for tuning).
-    if (!counters && decode_stream_supported(p) && getenv("DGX_ATTN_DECODE_STREAM"))
+    // One query token per sequence: the streaming decode kernel.
+    if (decode_stream_supported(p))
         return launch_decode_stream(p, chunk, part, st);
     if (p.NQ % p.NKV) return hipErrorInvalidValue;
     const int GRP = p.NQ / p.NKV;
@@ -483,7 +488,7 @@ hipError_t launch_split(const Problem &p, int chunk, const Partials &part, int *
     split_tiling(p, RB, tpb, nchunks);
     if (RB * 16 < GRP || RB > 4) return hipErrorInvalidValue;
     if (p.max_pos / chunk + 1 > part.ns_cap) return hipErrorInvalidValue;
-    SplitArgs a{p, part, chunk, tpb, nchunks, p.scale * kLog2e, counters};
+    SplitArgs a{p, part, chunk, tpb, nchunks, p.scale * kLog2e};
     dim3 grid(p.NKV, p.max_pos / chunk + 1, p.nseq * nchunks);
     if (grid.z > 65535u || grid.y > 65535u) return hipErrorInvalidConfiguration;
     const int kv = p.kv_dtype, q = p.q_dtype;

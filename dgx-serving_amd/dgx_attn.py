@@ -9,7 +9,7 @@ import os
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libdgx_attn.so")
+LIB_PATH = os.environ.get("DGX_ATTN_LIB") or os.path.join(_HERE, "libdgx_attn.so")   # override: alternate builds
 
 FP32, F16, BF16 = 0, 1, 2
 _DT = {torch.float32: FP32, torch.float16: F16, torch.bfloat16: BF16}
