@@ -1,27 +1,27 @@
-// Split-KV GQA attention for decode, verify and speculative tree verify on gfx950.
+// Split-KV GQA attention for verify, speculative tree verify and the decode shapes the streaming decode kernel
+// does not take (fp32 caches, HD 512, more than 16 query heads per KV head) on gfx950.
 //
 // Replaces the reference's attn_split_p1_kernel / attn_split_combine_kernel
 // (kernels/attention_decode_split.cuh:43-165) and, for short query runs, flash_attn2bs_p1(_custom)_kernel /
 // flash_attn2bs_p2_kernel (kernels/attention_flash.cuh:28-227).
 //
-// Grid: (chunk c, kv head, sequence x query-token tile). One workgroup = NW wave64s. It owns the query rows
-// (token, head) of one KV head (GQA group, rows token-major) for a token tile and the keys
-// [c*C, (c+1)*C) of its sequence, and writes one LSE partial per (row, chunk). Inside the chunk the keys are
-// cut into 32-key tiles at absolute positions; wave w takes tiles w, w+NW, ... and keeps its own online
-// softmax state in registers, so waves never synchronise until the end, where their states are merged in wave
-// order through LDS. Per tile a wave:
-//   * streams K (16 bytes per lane, straight into MFMA A fragments) and V (16-byte coalesced rows) from HBM,
-//   * computes S^T = K Q^T on 16x16x32 MFMA (Q fragments live in registers for the whole chunk),
-//   * applies the causal / sliding-window / tree mask and the online softmax on the S^T fragment (a query row
-//     sits in 4 lanes; row max and row sum are two xor shuffles),
-//   * stages the V tile in its private LDS slice and reads it back transposed as the A fragment of
-//     O^T += V^T P^T (P^T comes straight from the softmax registers, no LDS round trip).
+// Grid: (kv head, chunk c, sequence x query-token tile). One workgroup = 4 wave64s. It owns the query rows
+// (token, head) of one KV head (GQA group, rows token-major, RB blocks of 16) for a token tile and the keys
+// [c*C, (c+1)*C) of its sequence, and writes one LSE partial per (row, chunk). The chunk's keys stream in
+// 16-key tiles at absolute positions:
+//   * the workgroup fetches each K and V tile cooperatively with 16-byte loads (whole head rows),
+//     two tiles ahead in registers, and stages it in a double-buffered LDS tile (one barrier per tile),
+//   * every wave computes S^T = K Q^T for all rows of the tile on 16x16x32 MFMA (Q fragments in registers when
+//     they fit, else from LDS), applies the causal / sliding-window / tree mask and the online softmax on the
+//     S^T fragment (a query row sits in 4 lanes; row max and row sum are two xor shuffles),
+//   * wave w accumulates O^T += V^T P^T for head dims [w*HD/4, (w+1)*HD/4) on 16x16x16 MFMA, V^T fragments read
+//     with the gfx950 transpose read (ds_read_b64_tr_b16), P^T straight from the softmax registers.
 // Every K/V byte of a chunk is read once per workgroup and serves all GRP query heads of the KV head.
 //
 // Invariants (kept from the reference, attention_decode_split.cuh:8-12): chunk and tile boundaries are absolute
-// key positions; which wave owns a tile depends only on the tile's position; the partial merge and the chunk
-// combine run in fixed order. A row's result therefore does not depend on the batch, the other rows of its tile,
-// the grid size or the maximum position: a row is bit-identical alone (S=1), as a verify row or as a batch row.
+// key positions and the chunk combine runs in fixed order. A row's result therefore does not depend on the
+// batch, the other rows of its tile, the grid size or the maximum position: a row is bit-identical alone (S=1),
+// as a verify row or as a batch row.
 #include "attn_device.h"
 #include "attn_internal.h"
 #include <climits>
@@ -119,26 +119,17 @@ __device__ __forceinline__ void combine_wave(const Problem &p, const Partials &p
     if (p.lse && lane == 0) p.lse[(size_t)r * p.NQ + h] = (L > 0.f) ? (mg + log2f(L)) * kLn2 : kNegInf;
 }
 
-#ifndef DGX_SPLIT_STAGES
-#define DGX_SPLIT_STAGES 2
-#endif
-#ifndef DGX_SPLIT_NW
-#define DGX_SPLIT_NW 4
-#endif
-#ifndef DGX_SPLIT_KT
-#define DGX_SPLIT_KT 16
-#endif
 template <int HD, int RB>
 struct SplitCfg {
-    static constexpr int NW = DGX_SPLIT_NW;   // waves per workgroup; wave w owns head dims [w*HD/NW, (w+1)*HD/NW)
-    static constexpr int KT = DGX_SPLIT_KT;   // keys per tile (KT/16 sub-tiles of 16 keys)
+    static constexpr int NW = 4;              // waves per workgroup; wave w owns head dims [w*HD/NW, (w+1)*HD/NW)
+    static constexpr int KT = 16;             // keys per tile (KT/16 sub-tiles of 16 keys)
     static constexpr int NSUB = KT / 16;
     static constexpr int KS = HD / 32;        // QK k-steps (16x16x32)
     static constexpr int DBW = HD / 16 / NW;  // PV output dim blocks (16x16x16) per wave
     static constexpr int STR = HD + 8;        // LDS row stride of Q, K and V tiles (16-bit elements)
     static constexpr int RR = RB * 16;        // query rows per workgroup
     static constexpr int CPT = KT * HD / 8 / (NW * 64);   // 16-byte chunks per thread per tile (K and V each)
-    static constexpr int NSTG = DGX_SPLIT_STAGES;        // register stages of the K/V stream
+    static constexpr int NSTG = 2;                          // register stages of the K/V stream
     static constexpr size_t TILE = (size_t)KT * STR;      // elements of one K or V tile
     static constexpr bool QREG = RB * KS <= 8;            // Q fragments live in registers (straight from HBM)
     static constexpr size_t LDS = ((QREG ? 0 : (size_t)RR * STR) + 4 * TILE) * 2;   // [Q] + (K, V) x double buffer
@@ -441,10 +432,8 @@ static hipError_t dispatch_rb(const SplitArgs &a, int RB, dim3 grid, hipStream_t
     switch (RB) {
     case 1: return launch_split_t<HD, 1, KVT, QT>(a, grid, st);
     case 2: return launch_split_t<HD, 2, KVT, QT>(a, grid, st);
-#ifndef DGX_SPLIT_EXPERIMENT
     case 3: return launch_split_t<HD, 3, KVT, QT>(a, grid, st);
     case 4: return launch_split_t<HD, 4, KVT, QT>(a, grid, st);
-#endif
     default: return hipErrorInvalidValue;
     }
 }
@@ -452,10 +441,8 @@ static hipError_t dispatch_rb(const SplitArgs &a, int RB, dim3 grid, hipStream_t
 template <int KVT, int QT>
 static hipError_t dispatch_hd(const SplitArgs &a, int RB, dim3 grid, hipStream_t st) {
     switch (a.p.HD) {
-#ifndef DGX_SPLIT_EXPERIMENT
     case 128: return dispatch_rb<128, KVT, QT>(a, RB, grid, st);
     case 512: return dispatch_rb<512, KVT, QT>(a, RB, grid, st);
-#endif
     case 256: return dispatch_rb<256, KVT, QT>(a, RB, grid, st);
     default: return hipErrorInvalidValue;
     }
