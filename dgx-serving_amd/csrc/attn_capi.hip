@@ -132,9 +132,35 @@ Problem make_problem(const void *Q, int qt, const void *K, const void *V, int kv
     return p;
 }
 
+// ---------------------------------------------------------------- kernel timing (measurement hook)
+// With timing on, the main kernel of every split/decode and prefill launch is bracketed by a HIP event pair on
+// its launch stream (up to kTimed launches between reads).
+constexpr int kTimed = 4096;
+struct Timing {
+    bool on = false;
+    int n = 0;
+    hipEvent_t a[kTimed], b[kTimed];
+    bool made = false;
+};
+Timing g_timing;
+std::mutex g_timing_mu;
+
+template <class F>
+hipError_t timed_launch(hipStream_t st, F &&launch) {
+    int slot = -1;
+    if (g_timing.on) {
+        std::lock_guard<std::mutex> lk(g_timing_mu);
+        if (g_timing.n < kTimed) slot = g_timing.n++;
+    }
+    if (slot >= 0) { hipError_t e = hipEventRecord(g_timing.a[slot], st); if (e != hipSuccess) return e; }
+    hipError_t e = launch();
+    if (slot >= 0 && e == hipSuccess) e = hipEventRecord(g_timing.b[slot], st);
+    return e;
+}
+
 hipError_t run_split(const Problem &p, int chunk, Pool &pool, int ns_cap, hipStream_t st) {
     Partials part{pool.m, pool.l, pool.acc, ns_cap};
-    hipError_t e = launch_split(p, chunk, part, st);
+    hipError_t e = timed_launch(st, [&] { return launch_split(p, chunk, part, st); });
     if (e != hipSuccess) return e;
     return launch_combine(p, chunk, part, st);
 }
@@ -240,7 +266,7 @@ hipError_t dgx_flash_attn(const float *Q, const void *Kc, const void *Vc, int kv
     if (anc) return hipErrorInvalidValue;      // a tree mask covers at most 32 nodes (attention_flash.cuh:177)
     // No key split: the prefill kernel balances causal work by pairing query tiles, and a row's result does not
     // depend on how the prompt is chunked.
-    return launch_prefill(p, 0, Partials{nullptr, nullptr, nullptr, 0}, st);
+    return timed_launch(st, [&] { return launch_prefill(p, 0, Partials{nullptr, nullptr, nullptr, 0}, st); });
 }
 
 hipError_t dgx_flash_attn_v2(const float *Q, const void *Kc, const void *Vc, int kv_dtype, float *O, float *lse,
@@ -253,7 +279,7 @@ hipError_t dgx_flash_attn_v2(const float *Q, const void *Kc, const void *Vc, int
         return hipErrorInvalidValue;
     const Problem p = make_problem(Q, DT_FP32, Kc, Vc, kv_dtype, O, DT_FP32, lse, 1, Sq, NQ, NKV, HD, 0, 1, base, 1,
                                    nullptr, nullptr, base + Sq - 1, scale, window);
-    return launch_prefill(p, 0, Partials{nullptr, nullptr, nullptr, 0}, st);
+    return timed_launch(st, [&] { return launch_prefill(p, 0, Partials{nullptr, nullptr, nullptr, 0}, st); });
 }
 
 hipError_t dgx_attn(const float *Q, const float *K, const float *V, float *O, int S, int NQ, int NKV, int HD,
@@ -327,7 +353,39 @@ hipError_t dgx_attn_prefill(const void *Q, int q_dtype, const void *Kc, const vo
     const Problem p = make_problem(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, nseq, Sq, NQ, NKV, HD, kv_stride, 1,
                                    base, 1, base_b, nullptr, max_pos, scale, window);
     Partials part{pool->m, pool->l, pool->acc, ns};
-    return launch_prefill(p, kv_split, part, st);
+    return timed_launch(st, [&] { return launch_prefill(p, kv_split, part, st); });
+}
+
+hipError_t dgx_attn_timing(int on) {
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    if (on && !g_timing.made) {
+        for (int i = 0; i < kTimed; i++) {
+            hipError_t e = hipEventCreateWithFlags(&g_timing.a[i], hipEventDisableSystemFence);
+            if (e == hipSuccess) e = hipEventCreateWithFlags(&g_timing.b[i], hipEventDisableSystemFence);
+            if (e != hipSuccess) return e;
+        }
+        g_timing.made = true;
+    }
+    g_timing.on = on != 0;
+    g_timing.n = 0;
+    return hipSuccess;
+}
+
+hipError_t dgx_attn_timing_read(float *avg_ms, int *count) {
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    double sum = 0.0;
+    for (int i = 0; i < g_timing.n; i++) {
+        hipError_t e = hipEventSynchronize(g_timing.b[i]);
+        if (e != hipSuccess) return e;
+        float ms = 0.f;
+        e = hipEventElapsedTime(&ms, g_timing.a[i], g_timing.b[i]);
+        if (e != hipSuccess) return e;
+        sum += ms;
+    }
+    if (count) *count = g_timing.n;
+    if (avg_ms) *avg_ms = g_timing.n ? (float)(sum / g_timing.n) : 0.f;
+    g_timing.n = 0;
+    return hipSuccess;
 }
 
 const char *dgx_attn_version(void) { return "dgx-attn-mi355x 0.1 (gfx950)"; }

@@ -56,7 +56,7 @@ template <int HD>
 __device__ __forceinline__ void combine_wave(const Problem &p, const Partials &part, int C, int s, int t, int h) {
     constexpr int D4 = HD / 4;                       // 4-dim groups of a row
     constexpr int NP = (D4 + 63) / 64;               // passes of 64 lanes over the row
-    constexpr int NB = HD >= 512 ? 16 : 32;          // partial rows in flight per lane
+    constexpr int NB = 16;                           // partial rows in flight per lane (the chunks of 8K keys at 512)
     const int lane = threadIdx.x & 63;
     const int r = s * p.T + t;
     const int pos = tok_pos(p, s, t), lo = win_lo(pos, p.window);
@@ -404,9 +404,10 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
 }
 
 // LSE combine: one wave per (row, head).
+constexpr int kCombineWaves = 4;
 template <int HD>
-__global__ void __launch_bounds__(256) combine_kernel(const Problem p, const Partials part, int C) {
-    const int rh = blockIdx.x * 4 + (threadIdx.x >> 6);
+__global__ void __launch_bounds__(kCombineWaves * 64) combine_kernel(const Problem p, const Partials part, int C) {
+    const int rh = blockIdx.x * kCombineWaves + (threadIdx.x >> 6);
     if (rh >= p.nseq * p.T * p.NQ) return;
     const int r = rh / p.NQ, h = rh % p.NQ;
     combine_wave<HD>(p, part, C, r / p.T, r % p.T, h);
@@ -489,11 +490,11 @@ hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipSt
 
 hipError_t launch_combine(const Problem &p, int chunk, const Partials &part, hipStream_t st) {
     const int rows = p.nseq * p.T * p.NQ;
-    dim3 grid((rows + 3) / 4);
+    dim3 grid((rows + kCombineWaves - 1) / kCombineWaves), blk(kCombineWaves * 64);
     switch (p.HD) {
-    case 128: hipLaunchKernelGGL(combine_kernel<128>, grid, dim3(256), 0, st, p, part, chunk); break;
-    case 256: hipLaunchKernelGGL(combine_kernel<256>, grid, dim3(256), 0, st, p, part, chunk); break;
-    case 512: hipLaunchKernelGGL(combine_kernel<512>, grid, dim3(256), 0, st, p, part, chunk); break;
+    case 128: hipLaunchKernelGGL(combine_kernel<128>, grid, blk, 0, st, p, part, chunk); break;
+    case 256: hipLaunchKernelGGL(combine_kernel<256>, grid, blk, 0, st, p, part, chunk); break;
+    case 512: hipLaunchKernelGGL(combine_kernel<512>, grid, blk, 0, st, p, part, chunk); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -45,6 +45,8 @@ def lib():
             "dgx_attn_batch": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, P, I, I, P, F, I], I),
             "dgx_attn_prefill": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, I, I, P, F, I], I),
             "dgx_attn_version": ([], ctypes.c_char_p),
+            "dgx_attn_timing": ([I], I),
+            "dgx_attn_timing_read": ([P, P], I),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -144,6 +146,18 @@ def attn_prefill(Q, K, V, O, nseq, Sq, NQ, NKV, HD, base=0, base_b=None, kv_stri
     _ck(lib().dgx_attn_prefill(_ptr(Q), _DT[Q.dtype], _ptr(K), _ptr(V), kv_code(K), _ptr(O), _DT[O.dtype], _ptr(lse),
                                nseq, Sq, NQ, NKV, HD, _ptr(base_b), base, kv_stride, max_pos, kv_split, _stream(),
                                float(scale), window), "dgx_attn_prefill")
+
+
+def timing(on):
+    """Bracket the main kernel of every decode/prefill launch with HIP events (dgx_attn_timing)."""
+    _ck(lib().dgx_attn_timing(1 if on else 0), "dgx_attn_timing")
+
+
+def timing_read():
+    """(average kernel ms, launches) since the last read (dgx_attn_timing_read)."""
+    ms, n = ctypes.c_float(), ctypes.c_int()
+    _ck(lib().dgx_attn_timing_read(ctypes.addressof(ms), ctypes.addressof(n)), "dgx_attn_timing_read")
+    return ms.value, n.value
 
 
 def version():

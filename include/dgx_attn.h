@@ -124,6 +124,14 @@ hipError_t dgx_attn_prefill(const void *Q, int q_dtype, const void *Kc, const vo
                             int base, long kv_stride, int max_pos, int kv_split, hipStream_t st, float scale,
                             int window);
 
+/* Measurement hook (no counterpart in the reference; for benchmarks and profilers). With timing on, the main
+ * kernel of every decode/verify (split or streaming kernel, without the LSE combine) and every prefill launch is
+ * bracketed by a HIP event pair on its launch stream, for up to 4096 launches. dgx_attn_timing_read waits for the
+ * recorded launches and returns their average duration in ms and their count, then starts a new record.
+ * dgx_attn_timing(0) switches it off. Not for concurrent use from several threads. */
+hipError_t dgx_attn_timing(int on);
+hipError_t dgx_attn_timing_read(float *avg_ms, int *count);
+
 /* Library version string. */
 const char *dgx_attn_version(void);
 
