@@ -1,12 +1,12 @@
-// Streaming split-KV GQA decode on gfx950: one query token per sequence, HD 128 or 256, up to 16 q-heads per KV
-// head, 16-bit caches (the decode rows of kernels/attention_decode_split.cuh:43-145 and of the per-slot flash
+// Streaming split-KV GQA decode on gfx950: up to 16 query rows (tokens x q-heads) per KV head and sequence, HD
+// 128 or 256, 16-bit caches (the decode rows of kernels/attention_decode_split.cuh:43-145 and of the per-slot flash
 // decode at models/qwen35_batch.cu:165-167).
 //
 // Grid: one workgroup per (sequence, key chunk of C keys, kv head) that holds keys, enumerated on the device from
 // the positions, so the launched workgroups with work come first and spread over all CUs. A workgroup owns the
-// GRP query rows of one KV head and one chunk; its NW wave64s take the chunk's 16-key tiles round-robin (wave w:
-// tiles w, w+NW, ...) and run fully independent online softmaxes, merged in wave order at the end. The main loop
-// has no workgroup barrier:
+// query rows of one KV head and one chunk (RW blocks of 16 rows, token-major); its NKL key lanes of wave64s take
+// the chunk's 16-key tiles round-robin (lane kl: tiles kl, kl+NKL, ...) and run fully independent online
+// softmaxes, merged in key-lane order at the end. The main loop has no workgroup barrier:
 //   * K and V rows are streamed from HBM with 16-byte non-temporal loads, whole 512-byte head rows per half
 //     wave (the KV cache is read once per call: non-temporal loads sustain a higher HBM rate and leave the
 //     caches to the partials and Q),
@@ -32,18 +32,18 @@ struct DecodeArgs {
     float sl2;
 };
 
-template <int HD, int NW_>
+template <int HD, int NKL_, int RW_>
 struct DecodeCfg {
-    static constexpr int NW = NW_, KT = 16;
+    static constexpr int NKL = NKL_, RW = RW_, NW = NKL_ * RW_, KT = 16;
     static constexpr int KS = HD / 32;                 // 32-dim blocks (QK k-steps, V fragment loads)
     static constexpr int DB = HD / 16;                 // 16-dim output blocks
     static constexpr int QSTR = HD + 8;                // Q row stride in LDS (16-bit elements)
     static constexpr int BSTR = HD + 4;                // merge buffer row stride (floats)
     static constexpr int VSTR = HD + 8;                // V tile row stride in LDS (16-bit elements)
     static constexpr int VCH = KT * HD / 8 / 64;       // 16-byte V chunks per lane per tile
-    static constexpr size_t LDS_Q = (size_t)16 * QSTR * 2;
+    static constexpr size_t LDS_Q = (size_t)RW * 16 * QSTR * 2;
     static constexpr size_t LDS_V = (size_t)NW * KT * VSTR * 2;     // one private tile per wave (K, then V)
-    static constexpr size_t LDS_MERGE = ((size_t)2 * NW * 16 + (size_t)16 * BSTR) * 4;
+    static constexpr size_t LDS_MERGE = ((size_t)2 * NW * 16 + (size_t)RW * 16 * BSTR) * 4;
     static constexpr size_t LDS = LDS_Q + (LDS_V > LDS_MERGE ? LDS_V : LDS_MERGE);
 };
 
@@ -54,13 +54,13 @@ extern "C" hipError_t dgx_dtrace_read(void *host, size_t bytes) {
 }
 #endif
 
-template <int HD, int NW_, int KVT, int QT>
-__global__ void __launch_bounds__(NW_ * 64) decode_stream_kernel(const DecodeArgs a) {
+template <int HD, int NKL_, int RW_, int KVT, int QT>
+__global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const DecodeArgs a) {
 #ifdef DGX_TRACE
     const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
 #endif
-    using Cf = DecodeCfg<HD, NW_>;
-    constexpr int NW = Cf::NW, KT = Cf::KT;
+    using Cf = DecodeCfg<HD, NKL_, RW_>;
+    constexpr int NW = Cf::NW, NKL = Cf::NKL, RW = Cf::RW, KT = Cf::KT;
     constexpr bool F16 = OpIsF16<KVT>::value;
     using KE = typename Elem<KVT>::T;
     using QE = typename Elem<QT>::T;
@@ -79,9 +79,13 @@ __global__ void __launch_bounds__(NW_ * 64) decode_stream_kernel(const DecodeArg
         for (int s0 = 0; s0 < p.nseq; s0 += 64) {
             int n = 0, first = 0;
             if (s0 + lane_ < p.nseq) {
-                const int ps = tok_pos(p, s0 + lane_, 0);
-                first = win_lo(ps, p.window) / C;
-                n = max(0, min(ps / C, cmax) - first + 1);
+                int lo_s = INT_MAX, hi_s = 0;                  // key range of the sequence's tokens
+                for (int t = 0; t < p.T; t++) {
+                    const int ps = tok_pos(p, s0 + lane_, t);
+                    lo_s = min(lo_s, win_lo(ps, p.window)); hi_s = max(hi_s, ps + 1);
+                }
+                first = lo_s / C;
+                n = max(0, min((hi_s - 1) / C, cmax) - first + 1);
             }
             int incl = n;                                      // inclusive prefix sum over the 64 lanes
 #pragma unroll
@@ -101,12 +105,18 @@ __global__ void __launch_bounds__(NW_ * 64) decode_stream_kernel(const DecodeArg
         if (seq < 0) return;
     }
     const int kvh = (int)blockIdx.x % p.NKV;
-    const int GRP = p.NQ / p.NKV;
-    const int pos = tok_pos(p, seq, 0), lo = win_lo(pos, p.window), hi = pos + 1;
+    const int GRP = p.NQ / p.NKV, nrows = p.T * GRP;          // rows rho = token-major (token, head)
+    int lo = INT_MAX, hi = 0;
+    for (int t = 0; t < p.T; t++) {
+        const int ps = tok_pos(p, seq, t);
+        lo = min(lo, win_lo(ps, p.window)); hi = max(hi, ps + 1);
+    }
     const int j_lo = max(c * C, lo), j_hi = min(c * C + C, hi);
     if (j_lo >= j_hi) return;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, ln = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, ln = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kl = wave % NKL, rw = wave / NKL;                 // key lane, 16-row block
     const size_t krow = (size_t)p.NKV * HD;
     const KE *Kb = reinterpret_cast<const KE *>(p.K) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
     const KE *Vb = reinterpret_cast<const KE *>(p.V) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
@@ -115,32 +125,47 @@ __global__ void __launch_bounds__(NW_ * 64) decode_stream_kernel(const DecodeArg
     uint16_t *vs = reinterpret_cast<uint16_t *>(smem + Cf::LDS_Q) + (size_t)wave * KT * Cf::VSTR;   // reused by the merge
     uint16_t *kls = vs;                        // the K tile is consumed before the V tile lands in the same slice
 
-    // Q rows of the group (zero rows past GRP), requested first: the LDS store below then waits only for them.
-    constexpr int QCH = 16 * (HD / 8) / (NW * 64);
+    // Q rows of the workgroup (zero rows past the last), requested first: the LDS store below waits only for them.
+    constexpr int QCH = RW * 16 * (HD / 8) / (NW * 64);
+    static_assert(QCH >= 1 && (RW * 16 * (HD / 8)) % (NW * 64) == 0, "Q loads");
     auto qrow_of = [&](int u) { return (tid + NW * 64 * u) / (HD / 8); };
     auto qcol_of = [&](int u) { return ((tid + NW * 64 * u) % (HD / 8)) * 8; };
     u32x4 qv[QCH];
 #pragma unroll
     for (int u = 0; u < QCH; u++) {
         qv[u] = u32x4{0u, 0u, 0u, 0u};
-        if (qrow_of(u) < GRP)
-            qv[u] = load8_op<QT, F16>(reinterpret_cast<const QE *>(p.Q) + ((size_t)seq * p.NQ + kvh * GRP + qrow_of(u)) * HD + qcol_of(u));
+        const int rho = qrow_of(u);
+        if (rho < nrows)
+            qv[u] = load8_op<QT, F16>(reinterpret_cast<const QE *>(p.Q) +
+                                      ((size_t)(seq * p.T + rho / GRP) * p.NQ + kvh * GRP + rho % GRP) * HD + qcol_of(u));
     }
-    // This wave's tiles: k = k0 .. k1-1 with tile k at key c*C + KT*(wave + NW*k), the ones meeting [j_lo, j_hi).
+    // This wave's rows and the wave-uniform bounds of its unmasked fast path.
+    const int r_lo = rw * 16, r_hi = min(nrows, r_lo + 16);     // rows [r_lo, r_hi); none if r_lo >= nrows
+    int lo_max = 0, pos_min = INT_MAX;
+    for (int t = r_lo / GRP; r_lo < r_hi && t <= (r_hi - 1) / GRP; t++) {
+        const int ps = tok_pos(p, seq, t);
+        lo_max = max(lo_max, win_lo(ps, p.window)); pos_min = min(pos_min, ps);
+    }
+    if (p.anc) pos_min = min(pos_min, tok_pos(p, seq, 0) - 1);   // tree keys never take the fast path
+    // This wave's tiles: k = k0 .. k1-1 with tile k at key c*C + KT*(kl + NKL*k), the ones meeting [j_lo, j_hi).
     const int tb0 = j_lo / KT - c * (C / KT), tb1 = (j_hi - 1) / KT - c * (C / KT);   // tile range in the chunk
-    const int k0 = tb0 <= wave ? 0 : (tb0 - wave + NW - 1) / NW;
-    const int k1 = tb1 < wave ? 0 : (tb1 - wave) / NW + 1;
-    // Keys of a tile are attended without per-key tests when the tile lies inside [j_lo, j_hi) and below the tree.
-    const int full_hi = min(j_hi, p.anc ? pos : INT_MAX);
+    const int k0 = tb0 <= kl ? 0 : (tb0 - kl + NKL - 1) / NKL;
+    const int k1 = r_lo >= r_hi ? k0 : (tb1 < kl ? 0 : (tb1 - kl) / NKL + 1);
     // Loads of tile k (K straight into A fragments; V rows coalesced for the private LDS transpose).
+    // With RW > 1 the RW waves of a key lane read the same tiles: plain loads, so the L2 serves the repeats.
     auto load = [&](int k, u32x4 (&kf)[Cf::VCH], u32x4 (&vr)[Cf::VCH]) {
-        const int jt = c * C + KT * (wave + NW * k);
+        const int jt = c * C + KT * (kl + NKL * k);
 #pragma unroll
         for (int u = 0; u < Cf::VCH; u++) {      // whole rows, 16 bytes per lane; the last tile clamps to the last key
             const int q = lane + 64 * u, key = q / (HD / 8), col = (q % (HD / 8)) * 8;
             const size_t off = (size_t)min(jt + key, hi - 1) * krow + col;
-            kf[u] = load8_op_stream<KVT, F16>(Kb + off);
-            vr[u] = load8_op_stream<KVT, F16>(Vb + off);
+            if constexpr (RW == 1) {
+                kf[u] = load8_op_stream<KVT, F16>(Kb + off);
+                vr[u] = load8_op_stream<KVT, F16>(Vb + off);
+            } else {
+                kf[u] = load8_op<KVT, F16>(Kb + off);
+                vr[u] = load8_op<KVT, F16>(Vb + off);
+            }
         }
     };
     // PF + 1 register buffers: the loads of tiles k + 1 .. k + PF are in flight while tile k is computed (PF = 0:
@@ -152,17 +177,22 @@ __global__ void __launch_bounds__(NW_ * 64) decode_stream_kernel(const DecodeArg
 #pragma unroll
     for (int u = 0; u < QCH; u++) *reinterpret_cast<u32x4 *>(qs + qrow_of(u) * Cf::QSTR + qcol_of(u)) = qv[u];
     RowMask rm;
-    rm.pos = pos; rm.lo = lo; rm.valid = ln < GRP; rm.tree = p.anc != nullptr;
-    rm.anc = p.anc ? p.anc[seq] : 0u; rm.tb = pos;
+    {
+        const int rho = r_lo + ln;
+        rm.valid = rho < nrows;
+        const int t = rm.valid ? rho / GRP : 0;
+        rm.pos = tok_pos(p, seq, t); rm.lo = win_lo(rm.pos, p.window); rm.tree = p.anc != nullptr;
+        rm.anc = p.anc ? p.anc[seq * p.T + t] : 0u; rm.tb = tok_pos(p, seq, 0);
+    }
     __syncthreads();
 
     float m = kNegInf, l = 0.f;
     f32x4 acc[Cf::DB];
 #pragma unroll
     for (int db = 0; db < Cf::DB; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint16_t *qrow = qs + ln * Cf::QSTR + 8 * g;
+    const uint16_t *qrow = qs + (r_lo + ln) * Cf::QSTR + 8 * g;
     auto compute = [&](int k, const u32x4 (&kr)[Cf::VCH], const u32x4 (&vr)[Cf::VCH]) {
-        const int jt = c * C + KT * (wave + NW * k);
+        const int jt = c * C + KT * (kl + NKL * k);
         // K rows through the wave's LDS slice into MFMA A fragments (lane = key ln, 16 bytes of dims 32 ks + 8 g).
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -183,7 +213,7 @@ __global__ void __launch_bounds__(NW_ * 64) decode_stream_kernel(const DecodeArg
         const f32x4 s = (s0 + s1) * a.sl2;
         // Online softmax (log2 domain), lazily moved reference max; l is this lane's share of the row sum.
         float tv[4];
-        if (jt >= j_lo && jt + KT <= full_hi) {
+        if (jt >= j_lo && jt + KT <= j_hi && jt >= lo_max && jt + KT - 1 <= pos_min) {
 #pragma unroll
             for (int i = 0; i < 4; i++) tv[i] = s[i];
         } else {
@@ -243,19 +273,21 @@ __global__ void __launch_bounds__(NW_ * 64) decode_stream_kernel(const DecodeArg
     }
 #endif
 
-    // Merge the four wave states in wave order (LDS, over the V slices), then write the chunk partial of each row.
+    // Merge the NKL key-lane states of each row block in key-lane order (LDS, over the tile slices), then write the
+    // chunk partial of each row.
     __syncthreads();
     if (g == 0) { redm[wave * 16 + ln] = m; redl[wave * 16 + ln] = l; }
     __syncthreads();
     float M = kNegInf;
 #pragma unroll
-    for (int w = 0; w < NW; w++) M = fmaxf(M, redm[w * 16 + ln]);
+    for (int w = 0; w < NKL; w++) M = fmaxf(M, redm[(rw * NKL + w) * 16 + ln]);
     const float f = (m == kNegInf) ? 0.f : fast_exp2(m - M);
-    for (int w = 0; w < NW; w++) {
-        if (wave == w && ln < GRP) {
+    float *rbuf = buf + (size_t)rw * 16 * Cf::BSTR;
+    for (int w = 0; w < NKL; w++) {
+        if (kl == w && r_lo + ln < nrows) {
 #pragma unroll
             for (int db = 0; db < Cf::DB; db++) {
-                f32x4 *dst = reinterpret_cast<f32x4 *>(buf + ln * Cf::BSTR + 16 * db + 4 * g);
+                f32x4 *dst = reinterpret_cast<f32x4 *>(rbuf + ln * Cf::BSTR + 16 * db + 4 * g);
                 f32x4 v = acc[db] * f;
                 if (w > 0) v += *dst;
                 *dst = v;
@@ -264,47 +296,65 @@ __global__ void __launch_bounds__(NW_ * 64) decode_stream_kernel(const DecodeArg
         __syncthreads();
     }
     const int ns = a.part.ns_cap;
-    for (int idx = tid; idx < GRP * (HD / 4); idx += NW * 64) {
-        const int row = idx / (HD / 4), d4 = idx % (HD / 4);
-        const size_t pi = ((size_t)seq * p.NQ + kvh * GRP + row) * ns + c;
-        *reinterpret_cast<f32x4 *>(a.part.acc + pi * HD + 4 * d4) = *reinterpret_cast<const f32x4 *>(buf + row * Cf::BSTR + 4 * d4);
+    auto part_index = [&](int rho) {
+        return ((size_t)(seq * p.T + rho / GRP) * p.NQ + kvh * GRP + rho % GRP) * ns + c;
+    };
+    for (int idx = tid; idx < nrows * (HD / 4); idx += NW * 64) {
+        const int rho = idx / (HD / 4), d4 = idx % (HD / 4);
+        *reinterpret_cast<f32x4 *>(a.part.acc + part_index(rho) * HD + 4 * d4) =
+            *reinterpret_cast<const f32x4 *>(buf + (size_t)rho * Cf::BSTR + 4 * d4);
     }
-    if (tid < GRP) {
+    for (int rho = tid; rho < nrows; rho += NW * 64) {
+        const int rb = rho / 16, rl = rho % 16;
         float Mr = kNegInf;
-        for (int w = 0; w < NW; w++) Mr = fmaxf(Mr, redm[w * 16 + tid]);
+        for (int w = 0; w < NKL; w++) Mr = fmaxf(Mr, redm[(rb * NKL + w) * 16 + rl]);
         float L = 0.f;
         if (Mr != kNegInf)
-            for (int w = 0; w < NW; w++) {
-                const float mw = redm[w * 16 + tid];
-                if (mw != kNegInf) L += redl[w * 16 + tid] * fast_exp2(mw - Mr);
+            for (int w = 0; w < NKL; w++) {
+                const float mw = redm[(rb * NKL + w) * 16 + rl];
+                if (mw != kNegInf) L += redl[(rb * NKL + w) * 16 + rl] * fast_exp2(mw - Mr);
             }
-        const size_t pi = ((size_t)seq * p.NQ + kvh * GRP + tid) * ns + c;
-        a.part.m[pi] = Mr; a.part.l[pi] = L;
+        a.part.m[part_index(rho)] = Mr; a.part.l[part_index(rho)] = L;
     }
 }
 
-template <int HD, int KVT, int QT>
-static hipError_t launch_dec_t(const DecodeArgs &a, dim3 grid, int nw, hipStream_t st) {
-    switch (nw) {
-    case 1: hipLaunchKernelGGL((decode_stream_kernel<HD, 1, KVT, QT>), grid, dim3(64), (DecodeCfg<HD, 1>::LDS), st, a); break;
-    case 2: hipLaunchKernelGGL((decode_stream_kernel<HD, 2, KVT, QT>), grid, dim3(128), (DecodeCfg<HD, 2>::LDS), st, a); break;
-    case 4: hipLaunchKernelGGL((decode_stream_kernel<HD, 4, KVT, QT>), grid, dim3(256), (DecodeCfg<HD, 4>::LDS), st, a); break;
-    default: return hipErrorInvalidValue;
+template <int HD, int RW, int KVT, int QT>
+static hipError_t launch_dec_rw(const DecodeArgs &a, dim3 grid, hipStream_t st) {
+    constexpr int NKL = 2;
+    using Cf = DecodeCfg<HD, NKL, RW>;
+    static bool configured = false;
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_stream_kernel<HD, NKL, RW, KVT, QT>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cf::LDS);
+        if (e != hipSuccess) return e;
+        configured = true;
     }
+    hipLaunchKernelGGL((decode_stream_kernel<HD, NKL, RW, KVT, QT>), grid, dim3(Cf::NW * 64), Cf::LDS, st, a);
     return hipGetLastError();
 }
 
+template <int HD, int KVT, int QT>
+static hipError_t launch_dec_t(const DecodeArgs &a, dim3 grid, int rw, hipStream_t st) {
+    switch (rw) {
+    case 1: return launch_dec_rw<HD, 1, KVT, QT>(a, grid, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 template <int KVT, int QT>
-static hipError_t dec_dispatch_hd(const DecodeArgs &a, dim3 grid, int nw, hipStream_t st) {
+static hipError_t dec_dispatch_hd(const DecodeArgs &a, dim3 grid, int rw, hipStream_t st) {
     switch (a.p.HD) {
-    case 128: return launch_dec_t<128, KVT, QT>(a, grid, nw, st);
-    case 256: return launch_dec_t<256, KVT, QT>(a, grid, nw, st);
+    case 128: return launch_dec_t<128, KVT, QT>(a, grid, rw, st);
+    case 256: return launch_dec_t<256, KVT, QT>(a, grid, rw, st);
     default: return hipErrorNotSupported;
     }
 }
 
 bool decode_stream_supported(const Problem &p) {
-    return p.T == 1 && (p.HD == 128 || p.HD == 256) && p.NQ % p.NKV == 0 && p.NQ / p.NKV <= 16 &&
+    // One 16-row block (RW = 1). The kernel also runs RW = 2..4 row blocks, one wave each per key lane, but then
+    // the row waves re-read every tile, which measured slower than the cooperative split kernel on the B=16 x
+    // 8-token tree workload (205 vs 193 us), so those shapes go to the split kernel.
+    return p.T >= 1 && (p.HD == 128 || p.HD == 256) && p.NQ % p.NKV == 0 && p.T * (p.NQ / p.NKV) <= 16 &&
            p.kv_dtype != DT_FP32;
 }
 
@@ -316,12 +366,12 @@ hipError_t launch_decode_stream(const Problem &p, int chunk, const Partials &par
     const long long items = (long long)p.NKV * (p.max_pos / chunk + 1) * p.nseq;   // upper bound of the work items
     if (items > INT_MAX) return hipErrorInvalidConfiguration;
     dim3 grid((unsigned)items);
-    const int nw = 2;   // two waves per chunk: every chunk of the B=16 ragged batch is resident at once
+    const int rw = (p.T * (p.NQ / p.NKV) + 15) / 16;   // 16-row blocks, one wave each per key lane
     const int kv = p.kv_dtype, q = p.q_dtype;
-    if (kv == DT_F16 && q == DT_FP32) return dec_dispatch_hd<DT_F16, DT_FP32>(a, grid, nw, st);
-    if (kv == DT_F16 && q == DT_F16) return dec_dispatch_hd<DT_F16, DT_F16>(a, grid, nw, st);
-    if (kv == DT_BF16 && q == DT_FP32) return dec_dispatch_hd<DT_BF16, DT_FP32>(a, grid, nw, st);
-    if (kv == DT_BF16 && q == DT_BF16) return dec_dispatch_hd<DT_BF16, DT_BF16>(a, grid, nw, st);
+    if (kv == DT_F16 && q == DT_FP32) return dec_dispatch_hd<DT_F16, DT_FP32>(a, grid, rw, st);
+    if (kv == DT_F16 && q == DT_F16) return dec_dispatch_hd<DT_F16, DT_F16>(a, grid, rw, st);
+    if (kv == DT_BF16 && q == DT_FP32) return dec_dispatch_hd<DT_BF16, DT_FP32>(a, grid, rw, st);
+    if (kv == DT_BF16 && q == DT_BF16) return dec_dispatch_hd<DT_BF16, DT_BF16>(a, grid, rw, st);
     return hipErrorNotSupported;
 }
 

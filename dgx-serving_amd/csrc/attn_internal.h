@@ -47,7 +47,7 @@ __device__ __forceinline__ int win_lo(int pos, int window) {
 
 // Split-KV decode / verify / tree kernel (waves split the keys of a chunk, small query-row tiles).
 hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipStream_t st);
-// Streaming decode kernel for one query token per sequence (T == 1, HD 128/256, GRP <= 16, 16-bit cache);
+// Streaming decode kernel (T x GRP <= 16 rows per KV head, HD 128/256, 16-bit cache);
 // hipErrorNotSupported for other shapes. Writes chunk partials for launch_combine.
 bool decode_stream_supported(const Problem &p);
 hipError_t launch_decode_stream(const Problem &p, int chunk, const Partials &part, hipStream_t st);

@@ -467,7 +467,7 @@ size_t partial_rows(const Problem &p, int chunk) {
 
 hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipStream_t st) {
     if (chunk <= 0 || chunk % 16) return hipErrorInvalidValue;
-    // One query token per sequence: the streaming decode kernel.
+    // Up to 16 rows per KV head (one query token at GRP <= 16): the streaming decode kernel.
     if (decode_stream_supported(p))
         return launch_decode_stream(p, chunk, part, st);
     if (p.NQ % p.NKV) return hipErrorInvalidValue;
