@@ -177,22 +177,31 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
     const size_t krow = (size_t)p.NKV * HD;
     const KE *Kb = reinterpret_cast<const KE *>(p.K) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
     const KE *Vb = reinterpret_cast<const KE *>(p.V) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
-    constexpr bool QREG = Cf::QREG;
+    // Two wave layouts. RB == 1: every wave computes S for the 16 rows and owns HD/4 output dims of PV. RB >= 2: wave
+    // w owns row block w (all dims), so S and PV are not repeated across waves; waves past the last row block only
+    // fetch and stash.
+    constexpr bool ROWS = RB >= 2;
+    constexpr int RBW = ROWS ? 1 : RB;                          // row blocks held by a wave
+    constexpr int DBN = ROWS ? HD / 16 : Cf::DBW;               // 16-dim PV blocks of a wave
+    auto rbg = [&](int j) { return ROWS ? wave : j; };         // row block of a wave's j-th block
+    const int dim0 = ROWS ? 0 : wave * (HD / NW);               // first output dim of the wave
+    const bool active = !ROWS || wave < RB;
+    constexpr bool QREG = ROWS ? RBW * Cf::KS <= 8 : Cf::QREG;
     uint16_t *qs = reinterpret_cast<uint16_t *>(smem);
-    uint16_t *tiles = qs + (QREG ? 0 : (size_t)Cf::RR * Cf::STR);   // [buf][K | V][KT][STR]
+    uint16_t *tiles = qs + (Cf::QREG ? 0 : (size_t)Cf::RR * Cf::STR);   // [buf][K | V][KT][STR]
 
     // Q rows of the workgroup (row rho = token-major (token, head)) in the MFMA operand format: straight into
     // registers when they fit (lane (row ln, group g) holds dims 32 ks + 8 g ..), else through LDS.
-    u32x4 qreg[QREG ? RB : 1][QREG ? Cf::KS : 1];
+    u32x4 qreg[QREG ? RBW : 1][QREG ? Cf::KS : 1];
     if constexpr (QREG) {
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++) {
-            const int rho = rb * 16 + ln;
+        for (int j = 0; j < RBW; j++) {
+            const int rho = rbg(j) * 16 + ln;
             const bool ok = rho < nrows;
             const int t = tok0 + (ok ? rho / GRP : 0), h = kvh * GRP + (ok ? rho % GRP : 0);
             const QE *qrow = reinterpret_cast<const QE *>(p.Q) + ((size_t)(seq * p.T + t) * p.NQ + h) * HD + 8 * g;
 #pragma unroll
-            for (int ks = 0; ks < Cf::KS; ks++) qreg[rb][ks] = ok ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
+            for (int ks = 0; ks < Cf::KS; ks++) qreg[j][ks] = ok ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
         }
     } else {
         for (int i = tid; i < Cf::RR * (HD / 8); i += NW * 64) {
@@ -205,17 +214,17 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
             *reinterpret_cast<u32x4 *>(qs + rho * Cf::STR + col) = v;
         }
     }
-    RowMask rm[RB];
+    RowMask rm[RBW];
 #pragma unroll
-    for (int rb = 0; rb < RB; rb++) {
-        const int rho = rb * 16 + ln;
+    for (int j = 0; j < RBW; j++) {
+        const int rho = rbg(j) * 16 + ln;
         const bool valid = rho < nrows;
         const int t = tok0 + (valid ? rho / GRP : 0);
         const int ps = tok_pos(p, seq, t);
-        rm[rb].pos = ps; rm[rb].lo = win_lo(ps, p.window); rm[rb].valid = valid;
-        rm[rb].tree = p.anc != nullptr;
-        rm[rb].anc = p.anc ? p.anc[seq * p.T + t] : 0u;
-        rm[rb].tb = p.anc ? tok_pos(p, seq, 0) : 0;
+        rm[j].pos = ps; rm[j].lo = win_lo(ps, p.window); rm[j].valid = valid;
+        rm[j].tree = p.anc != nullptr;
+        rm[j].anc = p.anc ? p.anc[seq * p.T + t] : 0u;
+        rm[j].tb = p.anc ? tok_pos(p, seq, 0) : 0;
     }
 
     // Block-uniform bounds for the unmasked fast path: a tile is "full" when every valid row attends all its keys.
@@ -251,13 +260,13 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
         }
     };
 
-    float m[RB], l[RB], mnew[RB];
-    f32x4 acc[RB][Cf::DBW];
+    float m[RBW], l[RBW], mnew[RBW];
+    f32x4 acc[RBW][DBN];
 #pragma unroll
-    for (int rb = 0; rb < RB; rb++) {
+    for (int rb = 0; rb < RBW; rb++) {
         m[rb] = kNegInf; l[rb] = 0.f;
 #pragma unroll
-        for (int db = 0; db < Cf::DBW; db++) acc[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int db = 0; db < DBN; db++) acc[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     const int jb = (j_lo / Cf::KT) * Cf::KT;
     const int ntile = (j_hi - jb + Cf::KT - 1) / Cf::KT;
@@ -271,21 +280,21 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
         const uint16_t *kt = tiles + (size_t)(it & 1) * 2 * Cf::TILE, *vt = kt + Cf::TILE;
         // S^T[key][row] = K Q^T (every wave computes the whole tile), two independent MFMA chains per sub-tile.
         constexpr int NSUB = Cf::NSUB;
-        f32x4 s[NSUB][RB], s2[NSUB][RB];
+        f32x4 s[NSUB][RBW], s2[NSUB][RBW];
 #pragma unroll
         for (int sub = 0; sub < NSUB; sub++)
 #pragma unroll
-            for (int rb = 0; rb < RB; rb++) s[sub][rb] = s2[sub][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int rb = 0; rb < RBW; rb++) s[sub][rb] = s2[sub][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < Cf::KS; ks++) {
 #pragma unroll
             for (int sub = 0; sub < NSUB; sub++) {
                 const u32x4 kf = *reinterpret_cast<const u32x4 *>(kt + (16 * sub + ln) * Cf::STR + 32 * ks + 8 * g);
 #pragma unroll
-                for (int rb = 0; rb < RB; rb++) {
+                for (int rb = 0; rb < RBW; rb++) {
                     u32x4 qf;
                     if constexpr (QREG) qf = qreg[rb][ks];
-                    else qf = *reinterpret_cast<const u32x4 *>(qs + (rb * 16 + ln) * Cf::STR + 32 * ks + 8 * g);
+                    else qf = *reinterpret_cast<const u32x4 *>(qs + (rbg(rb) * 16 + ln) * Cf::STR + 32 * ks + 8 * g);
                     if (ks & 1) s2[sub][rb] = mfma16<F16>(kf, qf, s2[sub][rb]);
                     else s[sub][rb] = mfma16<F16>(kf, qf, s[sub][rb]);
                 }
@@ -295,11 +304,11 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
         // kRescaleThreshold). l holds this lane's share of the row sum; the four lanes of a row are added once,
         // after the loop.
         const bool full = jt >= j_lo && jt + Cf::KT <= j_hi && jt >= lo_max && jt + Cf::KT - 1 <= pos_min;
-        u32x2 pop[NSUB][RB];
-        float tv[NSUB][RB][4];
+        u32x2 pop[NSUB][RBW];
+        float tv[NSUB][RBW][4];
         bool need = false;
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++) {
+        for (int rb = 0; rb < RBW; rb++) {
             float mx = kNegInf;
 #pragma unroll
             for (int sub = 0; sub < NSUB; sub++) {
@@ -316,17 +325,17 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
         }
         if (__any(need)) {
 #pragma unroll
-            for (int rb = 0; rb < RB; rb++) {
+            for (int rb = 0; rb < RBW; rb++) {
                 const float alpha = (mnew[rb] == m[rb]) ? 1.f : fast_exp2(m[rb] - mnew[rb]);
                 l[rb] *= alpha; m[rb] = mnew[rb];
 #pragma unroll
-                for (int db = 0; db < Cf::DBW; db++) acc[rb][db] *= alpha;
+                for (int db = 0; db < DBN; db++) acc[rb][db] *= alpha;
             }
         }
 #pragma unroll
         for (int sub = 0; sub < NSUB; sub++)
 #pragma unroll
-            for (int rb = 0; rb < RB; rb++) {
+            for (int rb = 0; rb < RBW; rb++) {
                 float pv[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) { pv[i] = (tv[sub][rb][i] == kNegInf) ? 0.f : fast_exp2(tv[sub][rb][i] - m[rb]); l[rb] += pv[i]; }
@@ -335,12 +344,12 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
         // O^T[this wave's dims] += V^T P^T (16x16x16): the A fragment is a transposed LDS read of the V tile.
 #pragma unroll
         for (int sub = 0; sub < NSUB; sub++) {
-            const uint16_t *vtr = vt + (16 * sub + 4 * g + (ln >> 2)) * Cf::STR + wave * (HD / NW) + 4 * (ln & 3);
+            const uint16_t *vtr = vt + (16 * sub + 4 * g + (ln >> 2)) * Cf::STR + dim0 + 4 * (ln & 3);
 #pragma unroll
-            for (int db = 0; db < Cf::DBW; db++) {
+            for (int db = 0; db < DBN; db++) {
                 const u32x2 vop = lds_read_tr16(vtr + 16 * db);
 #pragma unroll
-                for (int rb = 0; rb < RB; rb++) acc[rb][db] = mfma16k16<F16>(vop, pop[sub][rb], acc[rb][db]);
+                for (int rb = 0; rb < RBW; rb++) acc[rb][db] = mfma16k16<F16>(vop, pop[sub][rb], acc[rb][db]);
             }
         }
     };
@@ -354,7 +363,7 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
 #pragma unroll
         for (int k = 0; k < NSTG; k++) {
             fetch(kst[k], vst[k], jb + Cf::KT * (it + k + NSTG));
-            compute(it + k);
+            if (active) compute(it + k);
             stash(kst[(k + 1) % NSTG], vst[(k + 1) % NSTG], (it + k + 1) & 1);
             __syncthreads();
         }
@@ -362,7 +371,7 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
 #pragma unroll
     for (int k = 0; k < NSTG; k++) {                            // the last ntile % NSTG tiles
         if (it + k < ntile) {
-            compute(it + k);
+            if (active) compute(it + k);
             stash(kst[(k + 1) % NSTG], vst[(k + 1) % NSTG], (it + k + 1) & 1);
             __syncthreads();
         }
@@ -381,23 +390,24 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
     }
 #endif
 #pragma unroll
-    for (int rb = 0; rb < RB; rb++) l[rb] = sum_over_groups(l[rb]);
+    for (int rb = 0; rb < RBW; rb++) l[rb] = sum_over_groups(l[rb]);
+    if (!active) return;
 
-    // Chunk partial: wave w writes its dims of every row; wave 0 writes (m, l). Lane (row ln, group g) holds
-    // O^T[dims w*HD/4 + 16*db + 4g + i][row].
+    // Chunk partial: a wave writes its dims of its rows (and (m, l): wave 0 of the dims split, every wave of the
+    // rows split). Lane (row ln, group g) holds O^T[dims dim0 + 16*db + 4g + i][row].
     const int NQ = p.NQ, ns = a.part.ns_cap;
 #pragma unroll
-    for (int rb = 0; rb < RB; rb++) {
-        const int row = rb * 16 + ln;
+    for (int rb = 0; rb < RBW; rb++) {
+        const int row = rbg(rb) * 16 + ln;
         if (row >= nrows) continue;
         const int r = seq * p.T + tok0 + row / GRP, h = kvh * GRP + row % GRP;
         const size_t pi = ((size_t)r * NQ + h) * ns + c;
 #pragma unroll
-        for (int db = 0; db < Cf::DBW; db++) {
-            float *dst = a.part.acc + pi * HD + wave * (HD / NW) + 16 * db + 4 * g;
+        for (int db = 0; db < DBN; db++) {
+            float *dst = a.part.acc + pi * HD + dim0 + 16 * db + 4 * g;
             *reinterpret_cast<f32x4 *>(dst) = acc[rb][db];
         }
-        if (wave == 0 && g == 0) {
+        if ((ROWS || wave == 0) && g == 0) {
             a.part.m[pi] = m[rb]; a.part.l[pi] = l[rb];
         }
     }
