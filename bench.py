@@ -129,7 +129,8 @@ def run_tree(steps, warmup, seed=5):
     ancd = torch.from_numpy(anc.reshape(-1).view(np.int32)).cuda()
     max_pos = int(committed.max()) + Tq - 1
     A.split_reserve(B * Tq, NQ, max_pos + 1, HD)
-    fn = lambda: A.attn_batch(Q, K, V, O, B, Tq, NQ, NKV, HD, base_b, ML * NKV * HD, max_pos, chunk=512, anc=ancd)
+    chunk = int(os.environ.get("BENCH_TREE_CHUNK", "512"))
+    fn = lambda: A.attn_batch(Q, K, V, O, B, Tq, NQ, NKV, HD, base_b, ML * NKV * HD, max_pos, chunk=chunk, anc=ancd)
     ms = timed(fn, steps, warmup)
     nbytes = int((committed + Tq).sum()) * NKV * HD * 4 + 2 * Q.numel() * 2
     return ms, nbytes
@@ -152,6 +153,27 @@ def run_sliding_decode(steps, warmup, seed=9):
     ms = timed(fn, steps, warmup)
     nbytes = B * W * NKV * HD * 4 + 2 * Q.numel() * 2
     return ms, nbytes
+
+
+def run_kv_append(steps, warmup, B=16, T=1, NKV=4, HD=256, ML=8192, kvdt=1):
+    """Ragged KV append of one decode step (Qwen3.5 shape): one dgx_kv_append launch vs the reference's per-slot
+    loop of 2B kv_store launches. Returns (fused ms, loop ms, algorithmic bytes)."""
+    row = NKV * HD
+    g = torch.Generator(device="cuda").manual_seed(9)
+    k = torch.randn(B * T * row, device="cuda", generator=g); v = torch.randn_like(k)
+    dt = {1: torch.float16, 2: torch.bfloat16}[kvdt]
+    Kc = torch.zeros(B * ML * row, device="cuda", dtype=dt); Vc = torch.zeros_like(Kc)
+    pos_h = np.random.default_rng(9).integers(0, ML - T, size=B).astype(np.int32)
+    pos = torch.from_numpy(pos_h).cuda()
+    fused = timed(lambda: A.kv_append(k, v, Kc, Vc, kvdt, B, T, ML * row, row, pos), steps, warmup)
+
+    def loop():
+        for b in range(B):
+            off = (b * ML + int(pos_h[b])) * row
+            A.kv_store(k[b * T * row:], Kc[off:], T * row, kvdt, 0)
+            A.kv_store(v[b * T * row:], Vc[off:], T * row, kvdt, 1)
+    looped = timed(loop, steps, warmup)
+    return fused, looped, B * T * row * (4 + 2) * 2
 
 
 def cpu_baseline(w):
@@ -227,6 +249,9 @@ def main():
         extra["prefill_sliding_T4096_w1024"] = dict(us=round(sms * 1e3, 2), tflops=round(sfl / (sms * 1e-3) / 1e12, 2))
         dms, dby = run_sliding_decode(args.steps, args.warmup)
         extra["decode_sliding_B8_w1024"] = dict(us=round(dms * 1e3, 2), gbs=round(dby / (dms * 1e-3) / 1e9, 1))
+        ams, lms, aby = run_kv_append(args.steps, args.warmup)
+        extra["kv_append_B16"] = dict(us=round(ams * 1e3, 2), per_slot_loop_us=round(lms * 1e3, 2),
+                                      gbs=round(aby / (ams * 1e-3) / 1e9, 1))
         tms, tby = run_tree(args.steps, args.warmup)
         extra["tree_verify_B16x8"] = dict(us=round(tms * 1e3, 2), gbs=round(tby / (tms * 1e-3) / 1e9, 1))
     out = {

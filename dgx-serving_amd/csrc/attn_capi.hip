@@ -315,6 +315,14 @@ hipError_t dgx_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int
 }
 hipError_t dgx_kv_stats(unsigned out[4]) { return read_kv_stats(out); }
 
+hipError_t dgx_kv_append(const float *k_src, const float *v_src, void *Kc, void *Vc, int kv_dtype, int nseq, int T,
+                         long kv_stride, int row_elems, const int *pos_b, int base, hipStream_t st) {
+    if (nseq == 0 || T == 0) return hipSuccess;
+    if (!k_src || !v_src || !Kc || !Vc || !valid_dtype(kv_dtype)) return hipErrorInvalidValue;
+    return launch_kv_append(k_src, v_src, Kc, Vc, kv_dtype, nseq, T, kv_stride, row_elems, pos_b, base,
+                            knob_on("G4_KV_STATS") ? 1 : 0, st);
+}
+
 hipError_t dgx_attn_batch(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
                           int o_dtype, float *lse, int B, int Tq, int NQ, int NKV, int HD, const int *base_b, int base,
                           long kv_stride, const unsigned *anc, int max_pos, int chunk, hipStream_t st, float scale,

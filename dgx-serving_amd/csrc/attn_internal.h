@@ -70,6 +70,8 @@ hipError_t launch_scalar_rows(const float *Q, const float *Kc, const float *Vc, 
                               int window, int reverse, hipStream_t st);
 hipError_t launch_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int which, int stats,
                            hipStream_t st);
+hipError_t launch_kv_append(const float *ks, const float *vs, void *Kc, void *Vc, int kv_dtype, int nseq, int T,
+                            long kv_stride, int row, const int *pos_b, int base, int stats, hipStream_t st);
 hipError_t read_kv_stats(unsigned out[4]);
 
 }  // namespace dgx

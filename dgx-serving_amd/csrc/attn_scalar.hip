@@ -160,6 +160,60 @@ hipError_t launch_kv_store(const float *src, void *dst, size_t n, int kv_dtype, 
     return hipGetLastError();
 }
 
+// Ragged KV append: token t of sequence b (source row b*T + t of [nseq*T][row] fp32 K and V) goes to cache row
+// pos(b) + t of sequence b (cache element b*kv_stride + (pos(b) + t)*row), converted as kv_store_kernel does.
+// One thread per 4 consecutive elements (a 16-byte fp32 read); grid.y = 0 for K, 1 for V.
+template <int DT>
+__global__ void __launch_bounds__(256) kv_append_kernel(const float *ks, const float *vs, void *Kc, void *Vc, int T,
+                                                        long kv_stride, int row, const int *pos_b, int base,
+                                                        size_t groups, int stats) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= groups) return;
+    const int which = blockIdx.y;
+    const int gpr = row / 4;
+    const size_t r = i / gpr, c = (i % gpr) * 4;
+    const int b = (int)(r / T), t = (int)(r % T);
+    const size_t o = (size_t)b * kv_stride + (size_t)((pos_b ? pos_b[b] : base) + t) * row + c;
+    const f32x4 v = *reinterpret_cast<const f32x4 *>((which ? vs : ks) + r * row + c);
+    void *dst = which ? Vc : Kc;
+    if constexpr (DT == DT_FP32) {
+        *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(dst) + o) = v;
+    } else {
+        constexpr bool F16 = DT == DT_F16;
+        uint16_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) h[e] = f32_to_op(v[e], F16);
+        *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(dst) + o) =
+            u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+        if (stats) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float back = F16 ? f16_bits_to_f32(h[e]) : bf16_bits_to_f32(h[e]);
+                if (!isfinite(back)) atomicAdd(&g_kv_stats[which], 1u);
+                else atomicMax(&g_kv_stats[2 + which], __float_as_uint(fabsf(back)));
+            }
+        }
+    }
+}
+
+hipError_t launch_kv_append(const float *ks, const float *vs, void *Kc, void *Vc, int kv_dtype, int nseq, int T,
+                            long kv_stride, int row, const int *pos_b, int base, int stats, hipStream_t st) {
+    if (nseq == 0 || T == 0) return hipSuccess;
+    if (nseq < 0 || T < 0 || row <= 0 || row % 4 || kv_stride % 4 || kv_stride < 0 || base < 0)
+        return hipErrorInvalidValue;
+    const size_t groups = (size_t)nseq * T * (row / 4);
+    const size_t blocks = (groups + 255) / 256;
+    if (blocks > 0x7fffffffu) return hipErrorInvalidConfiguration;
+    const dim3 grid((unsigned)blocks, 2);
+    switch (kv_dtype) {
+    case DT_FP32: hipLaunchKernelGGL(kv_append_kernel<DT_FP32>, grid, dim3(256), 0, st, ks, vs, Kc, Vc, T, kv_stride, row, pos_b, base, groups, 0); break;
+    case DT_F16: hipLaunchKernelGGL(kv_append_kernel<DT_F16>, grid, dim3(256), 0, st, ks, vs, Kc, Vc, T, kv_stride, row, pos_b, base, groups, stats); break;
+    case DT_BF16: hipLaunchKernelGGL(kv_append_kernel<DT_BF16>, grid, dim3(256), 0, st, ks, vs, Kc, Vc, T, kv_stride, row, pos_b, base, groups, stats); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 hipError_t read_kv_stats(unsigned out[4]) {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_kv_stats), sizeof(unsigned) * 4, 0, hipMemcpyDeviceToHost);
 }

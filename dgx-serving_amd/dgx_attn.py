@@ -42,6 +42,7 @@ def lib():
             "dgx_attn_decode_batch": ([P, P, P, P, I, I, I, I, I, L64, P, F, I, P], I),
             "dgx_kv_store": ([P, P, S, I, I, P], I),
             "dgx_kv_stats": ([P], I),
+            "dgx_kv_append": ([P, P, P, P, I, I, I, L64, I, P, I, P], I),
             "dgx_attn_batch": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, P, I, I, P, F, I], I),
             "dgx_attn_prefill": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, I, I, P, F, I], I),
             "dgx_attn_version": ([], ctypes.c_char_p),
@@ -123,6 +124,11 @@ def attn_decode_batch(Q, K, V, O, B, NQ, NKV, HD, base, kv_stride, scale=0.0, wi
 
 def kv_store(src, dst, n, kv_dtype, which):
     _ck(lib().dgx_kv_store(_ptr(src), _ptr(dst), n, kv_dtype, which, _stream()), "dgx_kv_store")
+
+
+def kv_append(k_src, v_src, Kc, Vc, kv_dtype, nseq, T, kv_stride, row_elems, pos_b=None, base=0):
+    _ck(lib().dgx_kv_append(_ptr(k_src), _ptr(v_src), _ptr(Kc), _ptr(Vc), kv_dtype, nseq, T, kv_stride, row_elems,
+                            _ptr(pos_b), base, _stream()), "dgx_kv_append")
 
 
 def kv_stats():

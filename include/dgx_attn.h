@@ -102,6 +102,13 @@ hipError_t dgx_attn_decode_batch(const float *Q, const float *Kc, const float *V
 hipError_t dgx_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int which, hipStream_t st);
 /* Read the G4_KV_STATS counters {nonfinite K, nonfinite V, max|K| bits, max|V| bits} (kv_store.cuh:86-98). */
 hipError_t dgx_kv_stats(unsigned out[4]);
+/* Ragged KV append in one launch: token t of sequence b (rows b*T + t of k_src / v_src, fp32 [nseq*T][row_elems])
+ * is stored at cache row (pos_b ? pos_b[b] : base) + t of sequence b (element b*kv_stride + pos*row_elems), converted
+ * to kv_dtype exactly as dgx_kv_store does (same G4_KV_STATS counters). pos_b is a device array or null;
+ * row_elems (= NKV*HD) and kv_stride must be multiples of 4. Replaces the per-slot kv_store / launch_f32_to_bf16 /
+ * cudaMemcpy loops of the batch decoders, models/gemma4_batch.cu:160-171 and models/qwen35_batch.cu:159-162. */
+hipError_t dgx_kv_append(const float *k_src, const float *v_src, void *Kc, void *Vc, int kv_dtype, int nseq, int T,
+                         long kv_stride, int row_elems, const int *pos_b, int base, hipStream_t st);
 
 /* ---- native entry points (16-bit Q/O, one ragged launch, explicit chunking) ---- */
 

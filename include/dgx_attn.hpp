@@ -50,6 +50,14 @@ static inline void kv_store(const float *src, float *dst, size_t n, int which, h
     dgx_detail::check(dgx_kv_store(src, dst, n, g4_kv_dtype(), which, st), "kv_store");
 }
 
+// One-launch ragged append of B slots x T tokens (replaces the per-slot kv_store loops of models/gemma4_batch.cu:
+// 160-171 and models/qwen35_batch.cu:159-162); pos_b: device array of per-slot positions, or null for `base`.
+static inline void kv_append(const float *k, const float *v, float *Kc, float *Vc, int B, int T, long kv_stride,
+                             size_t kvdim, const int *pos_b, int base, hipStream_t st = 0) {
+    dgx_detail::check(dgx_kv_append(k, v, Kc, Vc, g4_kv_dtype(), B, T, kv_stride, (int)kvdim, pos_b, base, st),
+                      "kv_append");
+}
+
 // ---- kernels/attention.cuh:72-198 (fp32 caches)
 static inline void launch_attn(const float *Q, const float *K, const float *V, float *O, int S, int NQ, int NKV, int HD,
                                hipStream_t st = 0, float scale = 0.f, int window = 0) {
