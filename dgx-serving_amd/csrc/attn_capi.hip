@@ -129,6 +129,7 @@ Problem make_problem(const void *Q, int qt, const void *K, const void *V, int kv
     p.pos_mode = pos_mode; p.base = base; p.pos_step = pos_step; p.pos_arr = pos_arr;
     p.anc = reinterpret_cast<const uint32_t *>(anc); p.max_pos = max_pos;
     p.scale = resolve_scale(scale, HD); p.window = window < 0 ? 0 : window;
+    p.Kp = nullptr; p.Vp = nullptr; p.gate = nullptr; p.gate_dtype = DT_FP32;
     return p;
 }
 
@@ -339,6 +340,28 @@ hipError_t dgx_attn_batch(const void *Q, int q_dtype, const void *Kc, const void
     if ((size_t)B * Tq * NQ * ns > pool->cap || (size_t)B * Tq * NQ * ns * HD > pool->acc_cap) return hipErrorInvalidValue;
     const Problem p = make_problem(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, B, Tq, NQ, NKV, HD, kv_stride, 1, base,
                                    1, base_b, anc, max_pos, scale, window);
+    return run_split(p, C, *pool, ns, st);
+}
+
+hipError_t dgx_attn_batch_ex(const void *Q, int q_dtype, const void *Kc, const void *Vc, const void *const *Kp,
+                             const void *const *Vp, int kv_dtype, void *O, int o_dtype, float *lse, const void *gate,
+                             int gate_dtype, int B, int Tq, int NQ, int NKV, int HD, const int *base_b, int base,
+                             long kv_stride, const unsigned *anc, int max_pos, int chunk, hipStream_t st, float scale,
+                             int window) {
+    if (B == 0 || Tq == 0) return hipSuccess;
+    if ((!Kp) != (!Vp) || (!Kp && (!Kc || !Vc)) || (gate && !valid_dtype(gate_dtype))) return hipErrorInvalidValue;
+    if (!Q || !O || B < 0 || Tq < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || !valid_hd(HD) || max_pos < 0 ||
+        !valid_dtype(q_dtype) || !valid_dtype(o_dtype) || kv_dtype == DT_FP32 || !valid_dtype(kv_dtype))
+        return hipErrorInvalidValue;
+    if (!Kp && B > 1 && kv_stride == 0 && !base_b) return hipErrorInvalidValue;
+    const int C = chunk > 0 ? chunk : dgx_attn_split_chunk();
+    if (C <= 0 || C % 32) return hipErrorInvalidValue;
+    Pool *pool; hipError_t e = pool_for(g_split, pool); if (e != hipSuccess) return e;
+    const int ns = max_pos / C + 1;
+    if ((size_t)B * Tq * NQ * ns > pool->cap || (size_t)B * Tq * NQ * ns * HD > pool->acc_cap) return hipErrorInvalidValue;
+    Problem p = make_problem(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, B, Tq, NQ, NKV, HD, kv_stride, 1, base,
+                             1, base_b, anc, max_pos, scale, window);
+    p.Kp = Kp; p.Vp = Vp; p.gate = gate; p.gate_dtype = gate_dtype;
     return run_split(p, C, *pool, ns, st);
 }
 

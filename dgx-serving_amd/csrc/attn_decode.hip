@@ -118,8 +118,8 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kl = wave % NKL, rw = wave / NKL;                 // key lane, 16-row block
     const size_t krow = (size_t)p.NKV * HD;
-    const KE *Kb = reinterpret_cast<const KE *>(p.K) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
-    const KE *Vb = reinterpret_cast<const KE *>(p.V) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
+    const KE *Kb = kv_base<KE>(p, false, seq) + (size_t)kvh * HD;
+    const KE *Vb = kv_base<KE>(p, true, seq) + (size_t)kvh * HD;
     uint16_t *qs = reinterpret_cast<uint16_t *>(smem);
     float *redm = reinterpret_cast<float *>(smem + Cf::LDS_Q), *redl = redm + NW * 16, *buf = redl + NW * 16;
     uint16_t *vs = reinterpret_cast<uint16_t *>(smem + Cf::LDS_Q) + (size_t)wave * KT * Cf::VSTR;   // reused by the merge

@@ -24,7 +24,19 @@ struct Problem {
     int max_pos;                      // host-side upper bound of every position (sizes the split grid)
     float scale;                      // resolved (> 0)
     int window;
+    const void *const *Kp;            // optional device arrays of per-sequence K / V bases (override K, V + s*kv_stride)
+    const void *const *Vp;
+    const void *gate;                 // optional output gate [rows, NQ, HD]: O *= sigmoid(gate) (split path only)
+    int gate_dtype;
 };
+
+// K (v = false) or V cache base of sequence s.
+template <class KE>
+__device__ __forceinline__ const KE *kv_base(const Problem &p, bool v, int s) {
+    const void *const *tab = v ? p.Vp : p.Kp;
+    if (tab) return reinterpret_cast<const KE *>(tab[s]);
+    return reinterpret_cast<const KE *>(v ? p.V : p.K) + (size_t)s * p.kv_stride;
+}
 
 // Split-KV partials in scratch: index (r * NQ + h) * ns_cap + c; m and l in the log2 domain (m = max of
 // scale*log2(e)*q.k, l = sum of 2^(t - m)), acc = sum 2^(t - m) v, unnormalised.

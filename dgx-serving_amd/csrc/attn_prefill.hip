@@ -134,8 +134,8 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rg = wave / KG, kg = wave % KG;
     const size_t krow = (size_t)p.NKV * HD;
-    const KE *Kb = reinterpret_cast<const KE *>(p.K) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
-    const KE *Vb = reinterpret_cast<const KE *>(p.V) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
+    const KE *Kb = kv_base<KE>(p, false, seq) + (size_t)kvh * HD;
+    const KE *Vb = kv_base<KE>(p, true, seq) + (size_t)kvh * HD;
     // Prefill tokens are consecutive: token t of this sequence sits at position pbase + t.
     const int pbase = __builtin_amdgcn_readfirstlane(p.pos_arr ? p.pos_arr[seq] : p.base);
 #ifdef DGX_TRACE

@@ -105,8 +105,25 @@ __device__ __forceinline__ void combine_wave(const Problem &p, const Partials &p
             }
         }
         if (d4 < D4) {
-            const f32x4 o = acc * inv;
+            f32x4 o = acc * inv;
             const size_t oi = ((size_t)r * p.NQ + h) * HD + 4 * d4;
+            if (p.gate) {                                // output gate: o *= 1 / (1 + 2^(-g log2 e))
+                float gv[4];
+                if (p.gate_dtype == DT_FP32) {
+                    const f32x4 gg = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(p.gate) + oi);
+                    gv[0] = gg.x; gv[1] = gg.y; gv[2] = gg.z; gv[3] = gg.w;
+                } else {
+                    const u32x2 gw = *reinterpret_cast<const u32x2 *>(reinterpret_cast<const uint16_t *>(p.gate) + oi);
+                    const bool f16 = p.gate_dtype == DT_F16;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const uint16_t b16 = (uint16_t)(gw[e / 2] >> (16 * (e & 1)));
+                        gv[e] = f16 ? f16_bits_to_f32(b16) : bf16_bits_to_f32(b16);
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[e] *= 1.f / (1.f + fast_exp2(-gv[e] * kLog2e));
+            }
             if (p.o_dtype == DT_FP32) *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.O) + oi) = o;
             else {
                 const bool f16 = p.o_dtype == DT_F16;
@@ -175,8 +192,8 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, ln = lane & 15;
     const size_t krow = (size_t)p.NKV * HD;
-    const KE *Kb = reinterpret_cast<const KE *>(p.K) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
-    const KE *Vb = reinterpret_cast<const KE *>(p.V) + (size_t)seq * p.kv_stride + (size_t)kvh * HD;
+    const KE *Kb = kv_base<KE>(p, false, seq) + (size_t)kvh * HD;
+    const KE *Vb = kv_base<KE>(p, true, seq) + (size_t)kvh * HD;
     // Two wave layouts. RB == 1: every wave computes S for the 16 rows and owns HD/4 output dims of PV. RB >= 2: wave
     // w owns row block w (all dims), so S and PV are not repeated across waves; waves past the last row block only
     // fetch and stash.

@@ -123,6 +123,19 @@ hipError_t dgx_attn_batch(const void *Q, int q_dtype, const void *Kc, const void
                           int o_dtype, float *lse, int B, int Tq, int NQ, int NKV, int HD, const int *base_b, int base,
                           long kv_stride, const unsigned *anc, int max_pos, int chunk, hipStream_t st, float scale,
                           int window);
+/* dgx_attn_batch with two caller-side fusions for the Qwen callers (models/qwen35_batch.cu:165-167,333-335 and
+ * models/qwen35_decode.cu:165-166):
+ *   - Kp / Vp: device arrays of B per-slot K / V base pointers (each [max_len, NKV, HD]); when given they replace
+ *     Kc / Vc + b*kv_stride (Kc, Vc, kv_stride are then ignored), so slots need not share one allocation;
+ *   - gate: optional [B*Tq, NQ, HD] tensor of dtype gate_dtype; the output is multiplied by sigmoid(gate) in the
+ *     LSE combine (the reference's separate launch_gate_sigmoid(attn, gate) after attention).
+ * Same rows, positions and masks as dgx_attn_batch; a row's result is bit-identical to dgx_attn_batch's when Kp,
+ * Vp point at the same caches and gate is null. */
+hipError_t dgx_attn_batch_ex(const void *Q, int q_dtype, const void *Kc, const void *Vc, const void *const *Kp,
+                             const void *const *Vp, int kv_dtype, void *O, int o_dtype, float *lse, const void *gate,
+                             int gate_dtype, int B, int Tq, int NQ, int NKV, int HD, const int *base_b, int base,
+                             long kv_stride, const unsigned *anc, int max_pos, int chunk, hipStream_t st, float scale,
+                             int window);
 /* Prefill with explicit key split (kv_split = 0: none; else a multiple of 64, partials + combine for rows that
  * span splits) over nseq sequences of Sq tokens at (base_b ? base_b[s] : base) + i. Uses the flash scratch
  * (grown in the call when needed). Native form of launch_flash_attn_v2 (attention_flash_v2.cuh:284-292). */
