@@ -110,6 +110,13 @@ hipError_t pool_for(Pool *pools, Pool *&out) {
     return hipSuccess;
 }
 
+// A ring-buffer cache of kv_cap rows holds the sliding window of every row of a launch: the keys a launch reads
+// span at most window + T - 1 positions, and whole 64-key steps map to consecutive rows.
+bool ring_ok(int kv_cap, int window, int T) {
+    if (kv_cap == 0) return true;
+    return kv_cap > 0 && kv_cap % 64 == 0 && window > 0 && (long)window + T - 1 <= kv_cap;
+}
+
 float resolve_scale(float scale, int HD) { return scale > 0.f ? scale : 1.0f / sqrtf((float)HD); }
 
 bool valid_hd(int HD) { return HD == 128 || HD == 256 || HD == 512; }
@@ -129,7 +136,7 @@ Problem make_problem(const void *Q, int qt, const void *K, const void *V, int kv
     p.pos_mode = pos_mode; p.base = base; p.pos_step = pos_step; p.pos_arr = pos_arr;
     p.anc = reinterpret_cast<const uint32_t *>(anc); p.max_pos = max_pos;
     p.scale = resolve_scale(scale, HD); p.window = window < 0 ? 0 : window;
-    p.Kp = nullptr; p.Vp = nullptr; p.gate = nullptr; p.gate_dtype = DT_FP32;
+    p.Kp = nullptr; p.Vp = nullptr; p.gate = nullptr; p.gate_dtype = DT_FP32; p.kv_cap = 0;
     return p;
 }
 
@@ -347,9 +354,10 @@ hipError_t dgx_attn_batch_ex(const void *Q, int q_dtype, const void *Kc, const v
                              const void *const *Vp, int kv_dtype, void *O, int o_dtype, float *lse, const void *gate,
                              int gate_dtype, int B, int Tq, int NQ, int NKV, int HD, const int *base_b, int base,
                              long kv_stride, const unsigned *anc, int max_pos, int chunk, hipStream_t st, float scale,
-                             int window) {
+                             int window, int kv_cap) {
     if (B == 0 || Tq == 0) return hipSuccess;
     if ((!Kp) != (!Vp) || (!Kp && (!Kc || !Vc)) || (gate && !valid_dtype(gate_dtype))) return hipErrorInvalidValue;
+    if (!ring_ok(kv_cap, window, Tq)) return hipErrorInvalidValue;
     if (!Q || !O || B < 0 || Tq < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || !valid_hd(HD) || max_pos < 0 ||
         !valid_dtype(q_dtype) || !valid_dtype(o_dtype) || kv_dtype == DT_FP32 || !valid_dtype(kv_dtype))
         return hipErrorInvalidValue;
@@ -361,18 +369,18 @@ hipError_t dgx_attn_batch_ex(const void *Q, int q_dtype, const void *Kc, const v
     if ((size_t)B * Tq * NQ * ns > pool->cap || (size_t)B * Tq * NQ * ns * HD > pool->acc_cap) return hipErrorInvalidValue;
     Problem p = make_problem(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, B, Tq, NQ, NKV, HD, kv_stride, 1, base,
                              1, base_b, anc, max_pos, scale, window);
-    p.Kp = Kp; p.Vp = Vp; p.gate = gate; p.gate_dtype = gate_dtype;
+    p.Kp = Kp; p.Vp = Vp; p.gate = gate; p.gate_dtype = gate_dtype; p.kv_cap = kv_cap;
     return run_split(p, C, *pool, ns, st);
 }
 
-hipError_t dgx_attn_prefill(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
-                            int o_dtype, float *lse, int nseq, int Sq, int NQ, int NKV, int HD, const int *base_b,
-                            int base, long kv_stride, int max_pos, int kv_split, hipStream_t st, float scale,
-                            int window) {
+hipError_t dgx_attn_prefill_ex(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
+                               int o_dtype, float *lse, int nseq, int Sq, int NQ, int NKV, int HD, const int *base_b,
+                               int base, long kv_stride, int max_pos, int kv_split, hipStream_t st, float scale,
+                               int window, int kv_cap) {
     if (nseq == 0 || Sq == 0) return hipSuccess;
     if (!Q || !Kc || !Vc || !O || nseq < 0 || Sq < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || !valid_hd(HD) ||
         max_pos < 0 || !valid_dtype(q_dtype) || !valid_dtype(o_dtype) || !valid_dtype(kv_dtype) || kv_split < 0 ||
-        kv_split % 64)
+        kv_split % 64 || !ring_ok(kv_cap, window, Sq))
         return hipErrorInvalidValue;
     Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
     const int ns = kv_split > 0 ? max_pos / kv_split + 1 : 1;
@@ -381,10 +389,19 @@ hipError_t dgx_attn_prefill(const void *Q, int q_dtype, const void *Kc, const vo
         e = pool_grow(*pool, (size_t)nseq * Sq * NQ * ns, (size_t)HD);
         if (e != hipSuccess) return e;
     }
-    const Problem p = make_problem(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, nseq, Sq, NQ, NKV, HD, kv_stride, 1,
-                                   base, 1, base_b, nullptr, max_pos, scale, window);
+    Problem p = make_problem(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, nseq, Sq, NQ, NKV, HD, kv_stride, 1,
+                             base, 1, base_b, nullptr, max_pos, scale, window);
+    p.kv_cap = kv_cap;
     Partials part{pool->m, pool->l, pool->acc, ns};
     return timed_launch(st, [&] { return launch_prefill(p, kv_split, part, st); });
+}
+
+hipError_t dgx_attn_prefill(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
+                            int o_dtype, float *lse, int nseq, int Sq, int NQ, int NKV, int HD, const int *base_b,
+                            int base, long kv_stride, int max_pos, int kv_split, hipStream_t st, float scale,
+                            int window) {
+    return dgx_attn_prefill_ex(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, nseq, Sq, NQ, NKV, HD, base_b, base,
+                               kv_stride, max_pos, kv_split, st, scale, window, 0);
 }
 
 hipError_t dgx_attn_timing(int on) {

@@ -154,11 +154,11 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
     // Loads of tile k (K straight into A fragments; V rows coalesced for the private LDS transpose).
     // With RW > 1 the RW waves of a key lane read the same tiles: plain loads, so the L2 serves the repeats.
     auto load = [&](int k, u32x4 (&kf)[Cf::VCH], u32x4 (&vr)[Cf::VCH]) {
-        const int jt = c * C + KT * (kl + NKL * k);
+        const int jt = c * C + KT * (kl + NKL * k), jrow = key_row(p, jt);
 #pragma unroll
         for (int u = 0; u < Cf::VCH; u++) {      // whole rows, 16 bytes per lane; the last tile clamps to the last key
             const int q = lane + 64 * u, key = q / (HD / 8), col = (q % (HD / 8)) * 8;
-            const size_t off = (size_t)min(jt + key, hi - 1) * krow + col;
+            const size_t off = (size_t)(jrow + min(key, hi - 1 - jt)) * krow + col;
             if constexpr (RW == 1) {
                 kf[u] = load8_op_stream<KVT, F16>(Kb + off);
                 vr[u] = load8_op_stream<KVT, F16>(Vb + off);

@@ -28,7 +28,13 @@ struct Problem {
     const void *const *Vp;
     const void *gate;                 // optional output gate [rows, NQ, HD]: O *= sigmoid(gate) (split path only)
     int gate_dtype;
+    int kv_cap;                       // 0: key j in cache row j; > 0 (multiple of 64): ring buffer, row j % kv_cap
 };
+
+// Cache row of key j0, a multiple of 16: tiles of 16 (64 in prefill steps) keys never wrap inside a ring.
+__device__ __forceinline__ int key_row(const Problem &p, int j0) {
+    return p.kv_cap > 0 ? (int)((unsigned)j0 % (unsigned)p.kv_cap) : j0;
+}
 
 // K (v = false) or V cache base of sequence s.
 template <class KE>

@@ -173,8 +173,8 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
     auto issue = [&](int k) {
         const int s = s0 + k;
         unsigned char *kd = smem + (size_t)(k % NS) * Cf::STAGE, *vd = kd + Cf::HALF;
-        const char *ks = reinterpret_cast<const char *>(Kb) + (size_t)s * SK * krow_b;
-        const char *vs = reinterpret_cast<const char *>(Vb) + (size_t)s * SK * krow_b;
+        const char *ks = reinterpret_cast<const char *>(Kb) + (size_t)key_row(p, s * SK) * krow_b;
+        const char *vs = reinterpret_cast<const char *>(Vb) + (size_t)key_row(p, s * SK) * krow_b;
         const bool inside = s * SK + SK <= hi_b;
 #pragma unroll
         for (int u = 0; u < NLD; u++) {

@@ -259,10 +259,11 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
     constexpr int NSTG = Cf::NSTG;
     u32x4 kst[NSTG][Cf::CPT], vst[NSTG][Cf::CPT];
     auto fetch = [&](u32x4 (&kr)[Cf::CPT], u32x4 (&vr)[Cf::CPT], int jt) {
+        const int jrow = key_row(p, jt);
 #pragma unroll
         for (int u = 0; u < Cf::CPT; u++) {
             const int q = tid + NW * 64 * u, key = q / (HD / 8), col = (q % (HD / 8)) * 8;
-            const size_t off = (size_t)min(jt + key, hi_b - 1) * krow + col;
+            const size_t off = (size_t)(jrow + min(key, hi_b - 1 - jt)) * krow + col;
             kr[u] = load8_op<KVT, F16>(Kb + off);
             vr[u] = load8_op<KVT, F16>(Vb + off);
         }

@@ -44,7 +44,8 @@ def lib():
             "dgx_kv_stats": ([P], I),
             "dgx_kv_append": ([P, P, P, P, I, I, I, L64, I, P, I, P], I),
             "dgx_attn_batch": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, P, I, I, P, F, I], I),
-            "dgx_attn_batch_ex": ([P, I, P, P, P, P, I, P, I, P, P, I, I, I, I, I, I, P, I, L64, P, I, I, P, F, I], I),
+            "dgx_attn_batch_ex": ([P, I, P, P, P, P, I, P, I, P, P, I, I, I, I, I, I, P, I, L64, P, I, I, P, F, I, I], I),
+            "dgx_attn_prefill_ex": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, I, I, P, F, I, I], I),
             "dgx_attn_prefill": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, I, I, P, F, I], I),
             "dgx_attn_version": ([], ctypes.c_char_p),
             "dgx_attn_timing": ([I], I),
@@ -147,20 +148,25 @@ def attn_batch(Q, K, V, O, B, Tq, NQ, NKV, HD, base_b, kv_stride, max_pos, chunk
 
 
 def attn_batch_ex(Q, O, B, Tq, NQ, NKV, HD, base_b, max_pos, K=None, V=None, kv_stride=0, Kp=None, Vp=None,
-                  kv_dtype=None, gate=None, chunk=0, anc=None, base=0, scale=0.0, window=0, lse=None):
+                  kv_dtype=None, gate=None, chunk=0, anc=None, base=0, scale=0.0, window=0, lse=None, kv_cap=0):
     """dgx_attn_batch_ex: per-slot K/V base pointers (Kp, Vp: int64 device tensors of addresses) and/or an output
     gate multiplied in as sigmoid(gate)."""
     kvdt = kv_dtype if kv_dtype is not None else kv_code(K)
     _ck(lib().dgx_attn_batch_ex(_ptr(Q), _DT[Q.dtype], _ptr(K), _ptr(V), _ptr(Kp), _ptr(Vp), kvdt, _ptr(O),
                                 _DT[O.dtype], _ptr(lse), _ptr(gate), _DT[gate.dtype] if gate is not None else 0,
                                 B, Tq, NQ, NKV, HD, _ptr(base_b), base, kv_stride, _ptr(anc), max_pos, chunk,
-                                _stream(), float(scale), window), "dgx_attn_batch_ex")
+                                _stream(), float(scale), window, kv_cap), "dgx_attn_batch_ex")
 
 
 def attn_prefill(Q, K, V, O, nseq, Sq, NQ, NKV, HD, base=0, base_b=None, kv_stride=0, max_pos=None, kv_split=0,
-                 scale=0.0, window=0, lse=None):
+                 scale=0.0, window=0, lse=None, kv_cap=0):
     if max_pos is None:
         max_pos = base + Sq - 1
+    if kv_cap:
+        _ck(lib().dgx_attn_prefill_ex(_ptr(Q), _DT[Q.dtype], _ptr(K), _ptr(V), kv_code(K), _ptr(O), _DT[O.dtype],
+                                      _ptr(lse), nseq, Sq, NQ, NKV, HD, _ptr(base_b), base, kv_stride, max_pos,
+                                      kv_split, _stream(), float(scale), window, kv_cap), "dgx_attn_prefill_ex")
+        return
     _ck(lib().dgx_attn_prefill(_ptr(Q), _DT[Q.dtype], _ptr(K), _ptr(V), kv_code(K), _ptr(O), _DT[O.dtype], _ptr(lse),
                                nseq, Sq, NQ, NKV, HD, _ptr(base_b), base, kv_stride, max_pos, kv_split, _stream(),
                                float(scale), window), "dgx_attn_prefill")

@@ -129,13 +129,16 @@ hipError_t dgx_attn_batch(const void *Q, int q_dtype, const void *Kc, const void
  *     Kc / Vc + b*kv_stride (Kc, Vc, kv_stride are then ignored), so slots need not share one allocation;
  *   - gate: optional [B*Tq, NQ, HD] tensor of dtype gate_dtype; the output is multiplied by sigmoid(gate) in the
  *     LSE combine (the reference's separate launch_gate_sigmoid(attn, gate) after attention).
+ *   - kv_cap > 0: the caches are ring buffers of kv_cap rows (a multiple of 64) for a sliding window: key j lives in
+ *     row j % kv_cap (the sliding-window ring layout of runtime/decode_state_gemma4.h:9-16, kv_cap). Needs
+ *     window > 0 and window + Tq - 1 <= kv_cap, so the keys a launch reads never alias.
  * Same rows, positions and masks as dgx_attn_batch; a row's result is bit-identical to dgx_attn_batch's when Kp,
- * Vp point at the same caches and gate is null. */
+ * Vp point at the same caches, gate is null and kv_cap is 0 (or the ring holds the same keys). */
 hipError_t dgx_attn_batch_ex(const void *Q, int q_dtype, const void *Kc, const void *Vc, const void *const *Kp,
                              const void *const *Vp, int kv_dtype, void *O, int o_dtype, float *lse, const void *gate,
                              int gate_dtype, int B, int Tq, int NQ, int NKV, int HD, const int *base_b, int base,
                              long kv_stride, const unsigned *anc, int max_pos, int chunk, hipStream_t st, float scale,
-                             int window);
+                             int window, int kv_cap);
 /* Prefill with explicit key split (kv_split = 0: none; else a multiple of 64, partials + combine for rows that
  * span splits) over nseq sequences of Sq tokens at (base_b ? base_b[s] : base) + i. Uses the flash scratch
  * (grown in the call when needed). Native form of launch_flash_attn_v2 (attention_flash_v2.cuh:284-292). */
@@ -143,6 +146,12 @@ hipError_t dgx_attn_prefill(const void *Q, int q_dtype, const void *Kc, const vo
                             int o_dtype, float *lse, int nseq, int Sq, int NQ, int NKV, int HD, const int *base_b,
                             int base, long kv_stride, int max_pos, int kv_split, hipStream_t st, float scale,
                             int window);
+
+/* dgx_attn_prefill over ring-buffer caches (kv_cap as in dgx_attn_batch_ex; window + Sq - 1 <= kv_cap). */
+hipError_t dgx_attn_prefill_ex(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
+                               int o_dtype, float *lse, int nseq, int Sq, int NQ, int NKV, int HD, const int *base_b,
+                               int base, long kv_stride, int max_pos, int kv_split, hipStream_t st, float scale,
+                               int window, int kv_cap);
 
 /* Measurement hook (no counterpart in the reference; for benchmarks and profilers). With timing on, the main
  * kernel of every decode/verify (split or streaming kernel, without the LSE combine) and every prefill launch is
