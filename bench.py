@@ -214,7 +214,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "all"], default="all")
+    ap.add_argument("--only", choices=["decode", "prefill", "tree", "all"], default="all")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (scale reference for HBM byte counters)")
     args = ap.parse_args()
@@ -231,6 +231,12 @@ def main():
         for _ in range(5):
             dst.copy_(src)
         torch.cuda.synchronize()
+    if args.only == "tree":                   # the tree-verify workload alone (profiling); not the headline line
+        tms, tby = run_tree(args.steps, args.warmup)
+        print(json.dumps({"metric": "tree-verify attention GB/s (B16 x 8 draft tokens, L<=16K)",
+                          "value": round(tby / (tms * 1e-3) / 1e9, 1), "unit": "GB/s", "us_per_call": round(tms * 1e3, 2),
+                          "steps": args.steps, "warmup": args.warmup, "higher_is_better": True}))
+        return
     w = decode_workload()
     ms, nbytes, kms = run_decode(w, args.steps, args.warmup, chunk=int(os.environ.get("BENCH_DECODE_CHUNK", "512")),
                            copies=int(os.environ.get("BENCH_DECODE_COPIES", "3")))
