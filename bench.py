@@ -155,6 +155,18 @@ def run_sliding_decode(steps, warmup, seed=9):
     return ms, nbytes
 
 
+def run_decode_fp32(steps, warmup, w):
+    """The fp32-cache decode path (launch_attn_decode_batch semantics: fp32 Q/K/V/O, fp32 FMA) on the config-2
+    shape and lengths. Returns (ms, algorithmic bytes)."""
+    B, NQ, NKV, HD, ML = w["B"], w["NQ"], w["NKV"], w["HD"], w["ML"]
+    K = w["K"].float(); V = w["V"].float()
+    Q = w["Q"].float(); O = torch.empty_like(Q)
+    ms = timed(lambda: A.attn_decode_batch(Q, K, V, O, B, NQ, NKV, HD, 0, ML * NKV * HD, base_b=w["pos"]), steps,
+               warmup)
+    del K, V
+    return ms, int(w["lens"].sum()) * NKV * HD * 4 * 2 + 2 * B * NQ * HD * 4
+
+
 def run_kv_append(steps, warmup, B=16, T=1, NKV=4, HD=256, ML=8192, kvdt=1):
     """Ragged KV append of one decode step (Qwen3.5 shape): one dgx_kv_append launch vs the reference's per-slot
     loop of 2B kv_store launches. Returns (fused ms, loop ms, algorithmic bytes)."""
@@ -255,6 +267,8 @@ def main():
         extra["prefill_sliding_T4096_w1024"] = dict(us=round(sms * 1e3, 2), tflops=round(sfl / (sms * 1e-3) / 1e12, 2))
         dms, dby = run_sliding_decode(args.steps, args.warmup)
         extra["decode_sliding_B8_w1024"] = dict(us=round(dms * 1e3, 2), gbs=round(dby / (dms * 1e-3) / 1e9, 1))
+        fms, fby = run_decode_fp32(max(args.steps // 10, 5), 2, w)
+        extra["decode_fp32_B16"] = dict(us=round(fms * 1e3, 2), gbs=round(fby / (fms * 1e-3) / 1e9, 1))
         ams, lms, aby = run_kv_append(args.steps, args.warmup)
         extra["kv_append_B16"] = dict(us=round(ams * 1e3, 2), per_slot_loop_us=round(lms * 1e3, 2),
                                       gbs=round(aby / (ams * 1e-3) / 1e9, 1))

@@ -3,6 +3,7 @@
 #include "attn_device.h"
 #include "attn_internal.h"
 #include "../../include/dgx_attn.h"
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -173,6 +174,26 @@ hipError_t run_split(const Problem &p, int chunk, Pool &pool, int ns_cap, hipStr
     return launch_combine(p, chunk, part, st);
 }
 
+// fp32 caches, up to 16 rows per KV head, no reverse-order diagnostic: the fp32 MFMA streaming kernel + combine on
+// the given pool (grown here when `grow`, as the reference's flash path grows its scratch inside the call).
+constexpr int kF32Chunk = 512;
+bool f32_fast(const Problem &p) { return decode_f32_supported(p) && !knob_on("G4_ATTN_DIAG_REVERSE"); }
+hipError_t run_f32(const Problem &p, Pool &pool, bool grow, hipStream_t st) {
+    const int ns = p.max_pos / kF32Chunk + 1;
+    const size_t need = (size_t)p.nseq * p.T * p.NQ * ns;
+    if (grow) {
+        std::lock_guard<std::mutex> lock(g_pool_mu);
+        hipError_t e = pool_grow(pool, need, (size_t)p.HD);
+        if (e != hipSuccess) return e;
+    } else if (need > pool.cap || need * p.HD > pool.acc_cap) {
+        return hipErrorInvalidValue;
+    }
+    Partials part{pool.m, pool.l, pool.acc, ns};
+    hipError_t e = timed_launch(st, [&] { return launch_decode_f32(p, kF32Chunk, part, st); });
+    if (e != hipSuccess) return e;
+    return launch_combine(p, kF32Chunk, part, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -224,6 +245,10 @@ hipError_t dgx_attn_decode_split(const float *Q, const void *Kc, const void *Vc,
         return hipErrorInvalidValue;
     }
     if (kv_dtype == DT_FP32) {
+        const Problem pf = make_problem(Q, DT_FP32, Kc, Vc, DT_FP32, O, DT_FP32, lse, rows, 1, NQ, NKV, HD, kv_stride, 0,
+                                        base, pos_step, pos_arr, nullptr, max_pos, scale, window);
+        // (the reservation, made for the library chunk <= 512, always covers the streaming kernel's 512-key chunks)
+        if (f32_fast(pf)) return run_f32(pf, *pool, false, st);
         if (lse) return hipErrorInvalidValue;   // the fp32 path keeps the reference's outputs (O only)
         return launch_scalar_rows(Q, (const float *)Kc, (const float *)Vc, O, rows, NQ, NKV, HD, base, pos_step, pos_arr,
                                   kv_stride, resolve_scale(scale, HD), window, knob_on("G4_ATTN_DIAG_REVERSE") ? 1 : 0, st);
@@ -302,6 +327,14 @@ hipError_t dgx_attn_decode(const float *Q, const float *Kc, const float *Vc, flo
     if (Sq == 0) return hipSuccess;
     if (!Q || !Kc || !Vc || !O || Sq < 0 || base < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || HD <= 0 || HD > 512)
         return hipErrorInvalidValue;
+    if (valid_hd(HD)) {
+        const Problem p = make_problem(Q, DT_FP32, Kc, Vc, DT_FP32, O, DT_FP32, nullptr, 1, Sq, NQ, NKV, HD, 0, 1,
+                                       base, 1, nullptr, nullptr, base + Sq - 1, scale, window);
+        if (f32_fast(p)) {
+            Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
+            return run_f32(p, *pool, true, st);
+        }
+    }
     return launch_scalar_decode(Q, Kc, Vc, O, 1, Sq, NQ, NKV, HD, base, 0, nullptr, resolve_scale(scale, HD),
                                 window < 0 ? 0 : window, knob_on("G4_ATTN_DIAG_REVERSE") ? 1 : 0, st);
 }
@@ -312,6 +345,19 @@ hipError_t dgx_attn_decode_batch(const float *Q, const float *Kc, const float *V
     if (B == 0) return hipSuccess;
     if (!Q || !Kc || !Vc || !O || B < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || HD <= 0 || HD > 512)
         return hipErrorInvalidValue;
+    // The streaming kernel needs a host bound of the positions: `base` without base_b, else the cache capacity
+    // kv_stride / (NKV*HD) rows.
+    const long row = (long)NKV * HD;
+    const long cap_rows = kv_stride > 0 ? kv_stride / row : 0;
+    if (valid_hd(HD) && (!base_b || (cap_rows > 0 && cap_rows <= INT_MAX))) {
+        const int max_pos = base_b ? (int)cap_rows - 1 : base;
+        const Problem p = make_problem(Q, DT_FP32, Kc, Vc, DT_FP32, O, DT_FP32, nullptr, B, 1, NQ, NKV, HD, kv_stride, 1,
+                                       base, 1, base_b, nullptr, max_pos, scale, window);
+        if (f32_fast(p)) {
+            Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
+            return run_f32(p, *pool, true, st);
+        }
+    }
     return launch_scalar_decode(Q, Kc, Vc, O, B, 1, NQ, NKV, HD, base, kv_stride, base_b, resolve_scale(scale, HD),
                                 window < 0 ? 0 : window, knob_on("G4_ATTN_DIAG_REVERSE") ? 1 : 0, st);
 }

@@ -54,6 +54,42 @@ extern "C" hipError_t dgx_dtrace_read(void *host, size_t bytes) {
 }
 #endif
 
+// Work item blockIdx.x -> (sequence, chunk c, kv head blockIdx.x % NKV), enumerating only the chunks that hold keys
+// of the sequence's tokens (kv head fastest): the workgroups with work come first in launch order and the dispatcher
+// spreads them over all CUs; the tail of the upper-bound grid (false) exits at once.
+__device__ __forceinline__ bool find_item(const Problem &p, int C, int &seq, int &c) {
+    const int lane_ = threadIdx.x & 63, cmax = p.max_pos / C;
+    int rest = (int)blockIdx.x / p.NKV;
+    seq = -1; c = 0;
+    for (int s0 = 0; s0 < p.nseq; s0 += 64) {
+        int n = 0, first = 0;
+        if (s0 + lane_ < p.nseq) {
+            int lo_s = INT_MAX, hi_s = 0;                  // key range of the sequence's tokens
+            for (int t = 0; t < p.T; t++) {
+                const int ps = tok_pos(p, s0 + lane_, t);
+                lo_s = min(lo_s, win_lo(ps, p.window)); hi_s = max(hi_s, ps + 1);
+            }
+            first = lo_s / C;
+            n = max(0, min((hi_s - 1) / C, cmax) - first + 1);
+        }
+        int incl = n;                                      // inclusive prefix sum over the 64 lanes
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o);
+            if (lane_ >= o) incl += y;
+        }
+        const unsigned long long hit = __ballot(incl > rest);
+        if (hit) {
+            const int l = __builtin_ctzll(hit);
+            seq = s0 + l;
+            c = __shfl(first, l) + rest - (__shfl(incl, l) - __shfl(n, l));
+            return true;
+        }
+        rest -= __shfl(incl, 63);
+    }
+    return false;
+}
+
 template <int HD, int NKL_, int RW_, int KVT, int QT>
 __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const DecodeArgs a) {
 #ifdef DGX_TRACE
@@ -68,42 +104,8 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
 
     const Problem &p = a.p;
     const int C = a.C;
-    // Work item blockIdx.x -> (sequence, chunk, kv head), enumerating only the chunks that hold keys (kv head
-    // fastest): the workgroups with work come first in launch order and the dispatcher spreads them over all CUs;
-    // the tail of the upper-bound grid exits at once.
     int seq, c;
-    {
-        const int lane_ = threadIdx.x & 63, cmax = p.max_pos / C;
-        int rest = (int)blockIdx.x / p.NKV;
-        seq = -1; c = 0;
-        for (int s0 = 0; s0 < p.nseq; s0 += 64) {
-            int n = 0, first = 0;
-            if (s0 + lane_ < p.nseq) {
-                int lo_s = INT_MAX, hi_s = 0;                  // key range of the sequence's tokens
-                for (int t = 0; t < p.T; t++) {
-                    const int ps = tok_pos(p, s0 + lane_, t);
-                    lo_s = min(lo_s, win_lo(ps, p.window)); hi_s = max(hi_s, ps + 1);
-                }
-                first = lo_s / C;
-                n = max(0, min((hi_s - 1) / C, cmax) - first + 1);
-            }
-            int incl = n;                                      // inclusive prefix sum over the 64 lanes
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int y = __shfl_up(incl, o);
-                if (lane_ >= o) incl += y;
-            }
-            const unsigned long long hit = __ballot(incl > rest);
-            if (hit) {
-                const int l = __builtin_ctzll(hit);
-                seq = s0 + l;
-                c = __shfl(first, l) + rest - (__shfl(incl, l) - __shfl(n, l));
-                break;
-            }
-            rest -= __shfl(incl, 63);
-        }
-        if (seq < 0) return;
-    }
+    if (!find_item(p, C, seq, c)) return;
     const int kvh = (int)blockIdx.x % p.NKV;
     const int GRP = p.NQ / p.NKV, nrows = p.T * GRP;          // rows rho = token-major (token, head)
     int lo = INT_MAX, hi = 0;
@@ -373,6 +375,229 @@ hipError_t launch_decode_stream(const Problem &p, int chunk, const Partials &par
     if (kv == DT_BF16 && q == DT_FP32) return dec_dispatch_hd<DT_BF16, DT_FP32>(a, grid, rw, st);
     if (kv == DT_BF16 && q == DT_BF16) return dec_dispatch_hd<DT_BF16, DT_BF16>(a, grid, rw, st);
     return hipErrorNotSupported;
+}
+
+// ---------------------------------------------------------------- fp32 caches
+// The same streaming decode in fp32 end to end (fp32 Q, K, V, P and accumulators) for fp32 caches, the
+// reference's fp32 decode path (attention.cuh:120-198, attention_decode_split.cuh:228; its gate asks for a
+// normalised error below 1e-5): S^T = K Q^T and O^T += V^T P^T on the fp32 MFMA v_mfma_f32_16x16x4_f32.
+// Operands (16x16x4: A lane l holds A[l % 16][l / 16], B lane l holds B[l / 16][l % 16]):
+//   * QK k-step ks (4 head dims): lane (key/row ln, group g) holds dim 16 (ks / 4) + 4 g + ks % 4, so one 16-byte
+//     LDS read of K (and of Q) row ln at dims 16 kq + 4 g feeds four k-steps;
+//   * PV k-step kb (4 keys): lane group g holds key 4 g + kb, which is element kb of the lane's own S^T fragment,
+//     so P^T never moves; the V^T operand is V[4 g + kb][16 db + ln], one 4-byte LDS read.
+template <int HD>
+struct DecodeF32Cfg {
+    static constexpr int NKL = 2, NW = 2, KT = 16;
+    static constexpr int KQ = HD / 16;                 // 16-dim blocks (4 QK k-steps each; PV output blocks)
+    static constexpr int STR = HD + 4;                 // LDS row stride (floats)
+    static constexpr int VCH = KT * HD / 4 / 64;       // 16-byte chunks per lane per tile (K and V each)
+    static constexpr int BSTR = HD + 4;
+    static constexpr size_t LDS_Q = (size_t)16 * STR * 4;
+    static constexpr size_t LDS_V = (size_t)NW * KT * STR * 4;
+    static constexpr size_t LDS_MERGE = ((size_t)2 * NW * 16 + (size_t)16 * BSTR) * 4;
+    static constexpr size_t LDS = LDS_Q + (LDS_V > LDS_MERGE ? LDS_V : LDS_MERGE);
+};
+
+__device__ __forceinline__ f32x4 mfma4f32(float a, float b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int HD>
+__global__ void __launch_bounds__(128) decode_f32_kernel(const DecodeArgs a) {
+    using Cf = DecodeF32Cfg<HD>;
+    constexpr int NKL = Cf::NKL, NW = Cf::NW, KT = Cf::KT, KQ = Cf::KQ;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const Problem &p = a.p;
+    const int C = a.C;
+    int seq, c;
+    if (!find_item(p, C, seq, c)) return;
+    const int kvh = (int)blockIdx.x % p.NKV;
+    const int GRP = p.NQ / p.NKV, nrows = p.T * GRP;
+    int lo = INT_MAX, hi = 0;
+    for (int t = 0; t < p.T; t++) {
+        const int ps = tok_pos(p, seq, t);
+        lo = min(lo, win_lo(ps, p.window)); hi = max(hi, ps + 1);
+    }
+    const int j_lo = max(c * C, lo), j_hi = min(c * C + C, hi);
+    if (j_lo >= j_hi) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, ln = lane & 15;
+    const int kl = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const size_t krow = (size_t)p.NKV * HD;
+    const float *Kb = kv_base<float>(p, false, seq) + (size_t)kvh * HD;
+    const float *Vb = kv_base<float>(p, true, seq) + (size_t)kvh * HD;
+    float *qs = reinterpret_cast<float *>(smem);
+    float *redm = reinterpret_cast<float *>(smem + Cf::LDS_Q), *redl = redm + NW * 16, *buf = redl + NW * 16;
+    float *ts = reinterpret_cast<float *>(smem + Cf::LDS_Q) + (size_t)kl * KT * Cf::STR;   // K, then V, of a tile
+
+    // Q rows (zero past the last row) -> LDS.
+    const float *Qf = reinterpret_cast<const float *>(p.Q);
+    for (int i = tid; i < 16 * (HD / 4); i += NW * 64) {
+        const int rho = i / (HD / 4), col = (i % (HD / 4)) * 4;
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (rho < nrows)
+            v = *reinterpret_cast<const f32x4 *>(Qf + ((size_t)(seq * p.T + rho / GRP) * p.NQ + kvh * GRP + rho % GRP) * HD + col);
+        *reinterpret_cast<f32x4 *>(qs + rho * Cf::STR + col) = v;
+    }
+    int lo_max = 0, pos_min = INT_MAX;
+    for (int t = 0; t < p.T; t++) {
+        const int ps = tok_pos(p, seq, t);
+        lo_max = max(lo_max, win_lo(ps, p.window)); pos_min = min(pos_min, ps);
+    }
+    if (p.anc) pos_min = min(pos_min, tok_pos(p, seq, 0) - 1);
+    RowMask rm;
+    {
+        rm.valid = ln < nrows;
+        const int t = rm.valid ? ln / GRP : 0;
+        rm.pos = tok_pos(p, seq, t); rm.lo = win_lo(rm.pos, p.window); rm.tree = p.anc != nullptr;
+        rm.anc = p.anc ? p.anc[seq * p.T + t] : 0u; rm.tb = tok_pos(p, seq, 0);
+    }
+    __syncthreads();
+
+    const int tb0 = j_lo / KT - c * (C / KT), tb1 = (j_hi - 1) / KT - c * (C / KT);
+    const int k0 = tb0 <= kl ? 0 : (tb0 - kl + NKL - 1) / NKL;
+    const int k1 = tb1 < kl ? 0 : (tb1 - kl) / NKL + 1;
+    float m = kNegInf, l = 0.f;
+    f32x4 acc[KQ];
+#pragma unroll
+    for (int db = 0; db < KQ; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = k0; k < k1; k++) {
+        const int jt = c * C + KT * (kl + NKL * k), jrow = key_row(p, jt);
+        f32x4 kr[Cf::VCH], vr[Cf::VCH];
+#pragma unroll
+        for (int u = 0; u < Cf::VCH; u++) {    // whole rows, 16 bytes per lane; the last tile clamps to the last key
+            const int q = lane + 64 * u, key = q / (HD / 4), col = (q % (HD / 4)) * 4;
+            const size_t off = (size_t)(jrow + min(key, hi - 1 - jt)) * krow + col;
+            kr[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(Kb + off));
+            vr[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(Vb + off));
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int u = 0; u < Cf::VCH; u++) {
+            const int q = lane + 64 * u, key = q / (HD / 4), col = (q % (HD / 4)) * 4;
+            *reinterpret_cast<f32x4 *>(ts + key * Cf::STR + col) = kr[u];
+        }
+        __builtin_amdgcn_wave_barrier();
+        f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+        for (int kq = 0; kq < KQ; kq++) {
+            const f32x4 kf = *reinterpret_cast<const f32x4 *>(ts + ln * Cf::STR + 16 * kq + 4 * g);
+            const f32x4 qf = *reinterpret_cast<const f32x4 *>(qs + ln * Cf::STR + 16 * kq + 4 * g);
+            s0 = mfma4f32(kf.x, qf.x, s0); s1 = mfma4f32(kf.y, qf.y, s1);
+            s0 = mfma4f32(kf.z, qf.z, s0); s1 = mfma4f32(kf.w, qf.w, s1);
+        }
+        const f32x4 sc = (s0 + s1) * a.sl2;
+        float tv[4];
+        const bool full = jt >= j_lo && jt + KT <= j_hi && jt >= lo_max && jt + KT - 1 <= pos_min;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int key = jt + 4 * g + i;
+            tv[i] = (full || ((key >= j_lo) & (key < j_hi) & rm.attends(key))) ? sc[i] : kNegInf;
+        }
+        float mx = fmaxf(fmaxf(tv[0], tv[1]), fmaxf(tv[2], tv[3]));
+        mx = max_over_groups(mx);
+        const float mnew = (mx > m + kRescaleThreshold) ? mx : m;
+        if (__any(mnew != m)) {
+            const float alpha = (mnew == m) ? 1.f : fast_exp2(m - mnew);
+            l *= alpha; m = mnew;
+#pragma unroll
+            for (int db = 0; db < KQ; db++) acc[db] *= alpha;
+        }
+        float pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) pv[i] = fast_exp2(tv[i] - m);
+        if (m == kNegInf) pv[0] = pv[1] = pv[2] = pv[3] = 0.f;
+        l += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int u = 0; u < Cf::VCH; u++) {
+            const int q = lane + 64 * u, key = q / (HD / 4), col = (q % (HD / 4)) * 4;
+            *reinterpret_cast<f32x4 *>(ts + key * Cf::STR + col) = vr[u];
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int db = 0; db < KQ; db++)
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) acc[db] = mfma4f32(ts[(4 * g + kb) * Cf::STR + 16 * db + ln], pv[kb], acc[db]);
+    }
+    l = sum_over_groups(l);
+
+    // Merge the two key-lane states in key-lane order, then write the chunk partial of each row.
+    __syncthreads();
+    if (g == 0) { redm[kl * 16 + ln] = m; redl[kl * 16 + ln] = l; }
+    __syncthreads();
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NKL; w++) M = fmaxf(M, redm[w * 16 + ln]);
+    const float f = (m == kNegInf) ? 0.f : fast_exp2(m - M);
+    for (int w = 0; w < NKL; w++) {
+        if (kl == w && ln < nrows) {
+#pragma unroll
+            for (int db = 0; db < KQ; db++) {
+                f32x4 *dst = reinterpret_cast<f32x4 *>(buf + ln * Cf::BSTR + 16 * db + 4 * g);
+                f32x4 v = acc[db] * f;
+                if (w > 0) v += *dst;
+                *dst = v;
+            }
+        }
+        __syncthreads();
+    }
+    const int ns = a.part.ns_cap;
+    auto part_index = [&](int rho) {
+        return ((size_t)(seq * p.T + rho / GRP) * p.NQ + kvh * GRP + rho % GRP) * ns + c;
+    };
+    for (int idx = tid; idx < nrows * (HD / 4); idx += NW * 64) {
+        const int rho = idx / (HD / 4), d4 = idx % (HD / 4);
+        *reinterpret_cast<f32x4 *>(a.part.acc + part_index(rho) * HD + 4 * d4) =
+            *reinterpret_cast<const f32x4 *>(buf + (size_t)rho * Cf::BSTR + 4 * d4);
+    }
+    for (int rho = tid; rho < nrows; rho += NW * 64) {
+        float Mr = kNegInf;
+        for (int w = 0; w < NKL; w++) Mr = fmaxf(Mr, redm[w * 16 + rho]);
+        float L = 0.f;
+        if (Mr != kNegInf)
+            for (int w = 0; w < NKL; w++) {
+                const float mw = redm[w * 16 + rho];
+                if (mw != kNegInf) L += redl[w * 16 + rho] * fast_exp2(mw - Mr);
+            }
+        a.part.m[part_index(rho)] = Mr; a.part.l[part_index(rho)] = L;
+    }
+}
+
+bool decode_f32_supported(const Problem &p) {
+    return p.kv_dtype == DT_FP32 && p.q_dtype == DT_FP32 && (p.HD == 128 || p.HD == 256) && p.NQ % p.NKV == 0 &&
+           p.T * (p.NQ / p.NKV) <= 16;
+}
+
+hipError_t launch_decode_f32(const Problem &p, int chunk, const Partials &part, hipStream_t st) {
+    if (!decode_f32_supported(p)) return hipErrorNotSupported;
+    if (chunk <= 0 || chunk % 16) return hipErrorInvalidValue;
+    if (p.max_pos / chunk + 1 > part.ns_cap) return hipErrorInvalidValue;
+    DecodeArgs a{p, part, chunk, p.scale * kLog2e};
+    const long long items = (long long)p.NKV * (p.max_pos / chunk + 1) * p.nseq;
+    if (items > INT_MAX) return hipErrorInvalidConfiguration;
+    dim3 grid((unsigned)items);
+    if (p.HD == 128) {
+        static bool conf = false;
+        if (!conf) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_f32_kernel<128>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)DecodeF32Cfg<128>::LDS);
+            if (e != hipSuccess) return e;
+            conf = true;
+        }
+        hipLaunchKernelGGL(decode_f32_kernel<128>, grid, dim3(128), DecodeF32Cfg<128>::LDS, st, a);
+    } else {
+        static bool conf = false;
+        if (!conf) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_f32_kernel<256>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)DecodeF32Cfg<256>::LDS);
+            if (e != hipSuccess) return e;
+            conf = true;
+        }
+        hipLaunchKernelGGL(decode_f32_kernel<256>, grid, dim3(128), DecodeF32Cfg<256>::LDS, st, a);
+    }
+    return hipGetLastError();
 }
 
 }  // namespace dgx

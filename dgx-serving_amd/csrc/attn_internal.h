@@ -69,6 +69,9 @@ hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipSt
 // hipErrorNotSupported for other shapes. Writes chunk partials for launch_combine.
 bool decode_stream_supported(const Problem &p);
 hipError_t launch_decode_stream(const Problem &p, int chunk, const Partials &part, hipStream_t st);
+// The same in fp32 end to end (fp32 Q and cache, fp32 MFMA) for fp32 caches, HD 128/256, T x GRP <= 16.
+bool decode_f32_supported(const Problem &p);
+hipError_t launch_decode_f32(const Problem &p, int chunk, const Partials &part, hipStream_t st);
 // Flash prefill kernel (waves split query rows, K/V tiles shared through LDS). kv_split = 0: one pass per row
 // tile writing O directly; kv_split > 0: keys cut at absolute multiples of kv_split, partials + combine.
 hipError_t launch_prefill(const Problem &p, int kv_split, const Partials &part, hipStream_t st);
