@@ -319,6 +319,14 @@ hipError_t dgx_attn(const float *Q, const float *K, const float *V, float *O, in
                     hipStream_t st, float scale, int window) {
     if (S == 0) return hipSuccess;
     if (!Q || !K || !V || !O || S < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || HD <= 0 || HD > 512) return hipErrorInvalidValue;
+    if (valid_hd(HD)) {                                   // short prompts: query i attends keys 0..i
+        const Problem p = make_problem(Q, DT_FP32, K, V, DT_FP32, O, DT_FP32, nullptr, 1, S, NQ, NKV, HD, 0, 1, 0, 1,
+                                       nullptr, nullptr, S - 1, scale, window);
+        if (f32_fast(p)) {
+            Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
+            return run_f32(p, *pool, true, st);
+        }
+    }
     return launch_scalar_prefill(Q, K, V, O, S, NQ, NKV, HD, resolve_scale(scale, HD), window < 0 ? 0 : window, st);
 }
 
