@@ -17,6 +17,9 @@
 //   * wave w accumulates O^T += V^T P^T for head dims [w*HD/4, (w+1)*HD/4) on 16x16x16 MFMA, V^T fragments read
 //     with the gfx950 transpose read (ds_read_b64_tr_b16), P^T straight from the softmax registers.
 // Every K/V byte of a chunk is read once per workgroup and serves all GRP query heads of the KV head.
+// With 2-4 row blocks (RB >= 2) wave w instead owns row block w with all head dims, so no S or PV work is repeated
+// across waves. For 16-bit caches at HD 128/256 those shapes (verify and tree verify runs) go to verify_kernel,
+// the same layout fed by a four-stage direct-to-LDS ring (global_load_lds, no staging registers).
 //
 // Invariants (kept from the reference, attention_decode_split.cuh:8-12): chunk and tile boundaries are absolute
 // key positions and the chunk combine runs in fixed order. A row's result therefore does not depend on the
@@ -259,11 +262,12 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
     constexpr int NSTG = Cf::NSTG;
     u32x4 kst[NSTG][Cf::CPT], vst[NSTG][Cf::CPT];
     auto fetch = [&](u32x4 (&kr)[Cf::CPT], u32x4 (&vr)[Cf::CPT], int jt) {
-        const int jrow = key_row(p, jt);
+        // A tile past the last one re-reads the last (in a ring its row base is that of the last tile).
+        const int jc = min(jt, ((hi_b - 1) / Cf::KT) * Cf::KT), jrow = key_row(p, jc);
 #pragma unroll
         for (int u = 0; u < Cf::CPT; u++) {
             const int q = tid + NW * 64 * u, key = q / (HD / 8), col = (q % (HD / 8)) * 8;
-            const size_t off = (size_t)(jrow + min(key, hi_b - 1 - jt)) * krow + col;
+            const size_t off = (size_t)(jrow + min(key, hi_b - 1 - jc)) * krow + col;
             kr[u] = load8_op<KVT, F16>(Kb + off);
             vr[u] = load8_op<KVT, F16>(Vb + off);
         }
@@ -431,6 +435,174 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- verify / tree kernel (16-bit caches, 2-4 row blocks)
+// The rows-split layout of split_kernel with a deeper K/V stream: tiles go from HBM straight into an NS-stage LDS
+// ring with gfx950 direct-to-LDS loads (no staging registers, so more tiles in flight per workgroup at the same
+// occupancy), rows unpadded with their 16-byte slots XOR-swizzled by the key (swz below). Wave w owns row block w
+// (all head dims); the wave past the last row block only loads.
+__device__ __forceinline__ int vswz(int k) { return ((k & 3) << 1) | ((k >> 2) & 1) | (k & 8); }
+typedef __attribute__((address_space(3))) void vlds_void;
+typedef __attribute__((address_space(1))) void vglb_void;
+
+template <int HD>
+struct VerifyCfg {
+    static constexpr int NW = 4, KT = 16, NS = 4;   // 64 KB of LDS at HD 256: two workgroups per CU
+    static constexpr int KS = HD / 32, DB = HD / 16, SLOTS = HD / 8, ROWB = HD * 2;
+    static constexpr int TILE = KT * ROWB;               // bytes of one K (or V) tile
+    static constexpr int STAGE = 2 * TILE;
+    static constexpr int NLD = KT * SLOTS / (NW * 64);    // direct-to-LDS loads per thread per tile and tensor
+    static constexpr size_t LDS = (size_t)NS * STAGE;
+    static_assert(NLD >= 1 && (KT * SLOTS) % (NW * 64) == 0, "tile loads");
+};
+
+template <int HD, int RB, int KVT, int QT>
+__global__ void __launch_bounds__(256) verify_kernel(const SplitArgs a) {
+    using Cf = VerifyCfg<HD>;
+    constexpr int NS = Cf::NS, KT = Cf::KT, KS = Cf::KS, DB = Cf::DB, NLD = Cf::NLD, SLOTS = Cf::SLOTS;
+    constexpr int ROWB = Cf::ROWB;
+    constexpr bool F16 = OpIsF16<KVT>::value;
+    using KE = typename Elem<KVT>::T;
+    using QE = typename Elem<QT>::T;
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const Problem &p = a.p;
+    const int kvh = blockIdx.x, c = blockIdx.y;
+    const int seq = blockIdx.z / a.nchunks, tchunk = blockIdx.z % a.nchunks;
+    const int GRP = p.NQ / p.NKV;
+    const int tok0 = tchunk * a.tpb, tok1 = min(p.T, tok0 + a.tpb);
+    const int nrows = (tok1 - tok0) * GRP;
+    int lo_b = INT_MAX, hi_b = 0;
+    for (int t = tok0; t < tok1; t++) {
+        const int ps = tok_pos(p, seq, t);
+        lo_b = min(lo_b, win_lo(ps, p.window)); hi_b = max(hi_b, ps + 1);
+    }
+    const int C = a.C;
+    const int j_lo = max(c * C, lo_b), j_hi = min(c * C + C, hi_b);
+    if (j_lo >= j_hi) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, ln = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool active = wave < RB;
+    const size_t krow = (size_t)p.NKV * HD;
+    const KE *Kb = kv_base<KE>(p, false, seq) + (size_t)kvh * HD;
+    const KE *Vb = kv_base<KE>(p, true, seq) + (size_t)kvh * HD;
+
+    // This wave's rows (row block `wave`): Q fragments in registers, the row mask.
+    const int rho = wave * 16 + ln;
+    const bool valid = active && rho < nrows;
+    const int tq = tok0 + (valid ? rho / GRP : 0);
+    u32x4 qf[KS];
+    {
+        const QE *qrow = reinterpret_cast<const QE *>(p.Q) + ((size_t)(seq * p.T + tq) * p.NQ + kvh * GRP + (valid ? rho % GRP : 0)) * HD + 8 * g;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) qf[ks] = valid ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
+    }
+    RowMask rm;
+    rm.pos = tok_pos(p, seq, tq); rm.lo = win_lo(rm.pos, p.window); rm.valid = valid;
+    rm.tree = p.anc != nullptr; rm.anc = p.anc ? p.anc[seq * p.T + tq] : 0u; rm.tb = p.anc ? tok_pos(p, seq, 0) : 0;
+    int lo_max = 0, pos_min = INT_MAX;
+    for (int t = tok0; t < tok1; t++) {
+        const int ps = tok_pos(p, seq, t);
+        lo_max = max(lo_max, win_lo(ps, p.window)); pos_min = min(pos_min, ps);
+    }
+    if (p.anc) pos_min = min(pos_min, tok_pos(p, seq, 0) - 1);
+
+    // Tile k (keys jb + KT k ..) -> stage k % NS. Thread slot S of a tensor's tile holds the 16-byte column
+    // (S % SLOTS) ^ vswz(key) of key row S / SLOTS; keys past the end re-read the last key (they are masked)
+    // and tiles past the last re-read the last.
+    const int jb = (j_lo / KT) * KT;
+    const int ntile = (j_hi - jb + KT - 1) / KT;
+    auto issue = [&](int k) {
+        const int jt = min(jb + KT * k, ((hi_b - 1) / KT) * KT), jrow = key_row(p, jt);
+        unsigned char *kd = smem + (size_t)(k % NS) * Cf::STAGE, *vd = kd + Cf::TILE;
+#pragma unroll
+        for (int u = 0; u < NLD; u++) {
+            const int i = wave * NLD + u, S = i * 64 + lane, key = S / SLOTS;
+            const size_t off = (size_t)(jrow + min(key, hi_b - 1 - jt)) * krow + (size_t)(((S % SLOTS) ^ vswz(key)) * 8);
+            __builtin_amdgcn_global_load_lds((vglb_void *)(Kb + off), (vlds_void *)(kd + (size_t)i * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((vglb_void *)(Vb + off), (vlds_void *)(vd + (size_t)i * 1024), 16, 0, 0);
+        }
+    };
+    // Tiles past the last are issued too (stages never read), so every wait sees the same count.
+#pragma unroll
+    for (int k = 0; k < NS - 1; k++) issue(k);
+
+    float m = kNegInf, l = 0.f;
+    f32x4 acc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const unsigned lds0 = (unsigned)(uintptr_t)smem;
+    const int vr = 4 * g + (ln >> 2);
+    const unsigned kaddr = lds0 + ln * ROWB + ((g ^ vswz(ln)) << 4);
+    const unsigned vaddr = lds0 + Cf::TILE + vr * ROWB + 8 * (ln & 1) + ((((ln & 3) >> 1) ^ vswz(vr)) << 4);
+
+    for (int it = 0; it < ntile; it++) {
+        // Tile it landed (NS - 2 younger tiles may still fly); the barrier makes every wave's loads visible and
+        // frees the stage of tile it-1 for tile it+NS-1.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD * (NS - 2)) : "memory");
+        __syncthreads();
+        issue(it + NS - 1);
+        if (!active) continue;
+        const int jt = jb + KT * it;
+        const unsigned stage = (it % NS) * Cf::STAGE;
+        unsigned kb = kaddr + stage, vb = vaddr + stage;
+        asm volatile("" : "+v"(kb), "+v"(vb));
+        u32x4 kf[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) asm volatile("ds_read_b128 %0, %1" : "=v"(kf[ks]) : "v"(kb ^ (64u * ks)) : "memory");
+        if constexpr (KS == 8)
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3]), "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]), "+v"(kf[7])::"memory");
+        else
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3])::"memory");
+        f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            if (ks & 1) s1 = mfma16<F16>(kf[ks], qf[ks], s1);
+            else s0 = mfma16<F16>(kf[ks], qf[ks], s0);
+        }
+        const f32x4 sc = (s0 + s1) * a.sl2;
+        const bool full = jt >= j_lo && jt + KT <= j_hi && jt >= lo_max && jt + KT - 1 <= pos_min;
+        float tv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int key = jt + 4 * g + i;
+            tv[i] = (full || (key >= j_lo && key < j_hi && rm.attends(key))) ? sc[i] : kNegInf;
+        }
+        float mx = fmaxf(fmaxf(tv[0], tv[1]), fmaxf(tv[2], tv[3]));
+        mx = max_over_groups(mx);
+        const float mnew = (mx > m + kRescaleThreshold) ? mx : m;
+        if (__any(mnew != m)) {
+            const float alpha = (mnew == m) ? 1.f : fast_exp2(m - mnew);
+            l *= alpha; m = mnew;
+#pragma unroll
+            for (int db = 0; db < DB; db++) acc[db] *= alpha;
+        }
+        float pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) { pv[i] = (tv[i] == kNegInf) ? 0.f : fast_exp2(tv[i] - m); l += pv[i]; }
+        const u32x2 pop = u32x2{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3])};
+#pragma unroll
+        for (int d8 = 0; d8 < DB; d8 += 8) {
+            u32x2 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v[j]) : "v"(vb ^ (32u * (d8 + j))) : "memory");
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]),
+                         "+v"(v[5]), "+v"(v[6]), "+v"(v[7])::"memory");
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[d8 + j] = mfma16k16<F16>(v[j], pop, acc[d8 + j]);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");        // no load may land after the workgroup ends
+    l = sum_over_groups(l);
+    if (!valid) return;
+    const int r = seq * p.T + tq, h = kvh * GRP + rho % GRP;
+    const size_t pi = ((size_t)r * p.NQ + h) * a.part.ns_cap + c;
+#pragma unroll
+    for (int db = 0; db < DB; db++) *reinterpret_cast<f32x4 *>(a.part.acc + pi * HD + 16 * db + 4 * g) = acc[db];
+    if (g == 0) { a.part.m[pi] = m; a.part.l[pi] = l; }
+}
+
 // LSE combine: one wave per (row, head).
 constexpr int kCombineWaves = 4;
 template <int HD>
@@ -444,6 +616,18 @@ __global__ void __launch_bounds__(kCombineWaves * 64) combine_kernel(const Probl
 // ---------------------------------------------------------------- host side
 template <int HD, int RB, int KVT, int QT>
 static hipError_t launch_split_t(const SplitArgs &a, dim3 grid, hipStream_t st) {
+    if constexpr (RB >= 2 && HD <= 256 && KVT != DT_FP32) {
+        using Cf = VerifyCfg<HD>;
+        static bool configured_v = false;
+        if (!configured_v) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&verify_kernel<HD, RB, KVT, QT>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cf::LDS);
+            if (e != hipSuccess) return e;
+            configured_v = true;
+        }
+        hipLaunchKernelGGL((verify_kernel<HD, RB, KVT, QT>), grid, dim3(256), Cf::LDS, st, a);
+        return hipGetLastError();
+    }
     using Cf = SplitCfg<HD, RB>;
     static bool configured = false;
     if (!configured) {
