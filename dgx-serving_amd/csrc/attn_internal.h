@@ -49,6 +49,9 @@ __device__ __forceinline__ const KE *kv_base(const Problem &p, bool v, int s) {
 struct Partials {
     float *m, *l, *acc;
     int ns_cap;
+    // Set by launch_split when verify_kernel wrote the partials (seg_g > 0: its grid size, minimum run length and
+    // token tiling); 0 for partials indexed by absolute key chunk.
+    int seg_g = 0, seg_qmin = 0, seg_tpb = 0, seg_nchunks = 0;
 };
 
 // Position of token t of sequence s, and the first key of its sliding window.
@@ -64,7 +67,7 @@ __device__ __forceinline__ int win_lo(int pos, int window) {
 }
 
 // Split-KV decode / verify / tree kernel (waves split the keys of a chunk, small query-row tiles).
-hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipStream_t st);
+hipError_t launch_split(const Problem &p, int chunk, Partials &part, hipStream_t st);
 // Streaming decode kernel (T x GRP <= 16 rows per KV head, HD 128/256, 16-bit cache);
 // hipErrorNotSupported for other shapes. Writes chunk partials for launch_combine.
 bool decode_stream_supported(const Problem &p);

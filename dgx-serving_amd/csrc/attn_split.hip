@@ -19,14 +19,17 @@
 // Every K/V byte of a chunk is read once per workgroup and serves all GRP query heads of the KV head.
 // With 2-4 row blocks (RB >= 2) wave w instead owns row block w with all head dims, so no S or PV work is repeated
 // across waves. For 16-bit caches at HD 128/256 those shapes (verify and tree verify runs) go to verify_kernel,
-// the same layout fed by a four-stage direct-to-LDS ring (global_load_lds, no staging registers).
+// the same layout fed by a four-stage direct-to-LDS ring (global_load_lds, no staging registers) over a grid of
+// resident workgroups that each stream an equal run of key tiles (see seg_scan).
 //
-// Invariants (kept from the reference, attention_decode_split.cuh:8-12): chunk and tile boundaries are absolute
-// key positions and the chunk combine runs in fixed order. A row's result therefore does not depend on the
-// batch, the other rows of its tile, the grid size or the maximum position: a row is bit-identical alone (S=1),
-// as a verify row or as a batch row.
+// Invariants (kept from the reference, attention_decode_split.cuh:8-12) for split_kernel: chunk and tile
+// boundaries are absolute key positions and the chunk combine runs in fixed order. A row's result therefore does
+// not depend on the batch, the other rows of its tile, the grid size or the maximum position: a row is
+// bit-identical alone or as a batch row. verify_kernel gives up the batch independence for the equal runs (its
+// run boundaries follow the total key count); its results are deterministic for given inputs.
 #include "attn_device.h"
 #include "attn_internal.h"
+#include <algorithm>
 #include <climits>
 #include <cstdlib>
 
@@ -51,6 +54,68 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Work split of verify_kernel. The key tiles of every (token tile z, KV head) pair, in the order (z, KV head, tile),
+// are cut into equal runs of q tiles, one run per workgroup of a grid of resident workgroups, so every workgroup
+// streams the same number of bytes whatever the mix of sequence lengths (a grid of fixed key chunks leaves a
+// partly filled last round of workgroups). A run writes one partial per pair it meets, into slot (workgroup index
+// - index of the pair's first workgroup); the combine derives the same slots from the positions. q depends on the
+// total tile count, so verify results depend on the batch; they are deterministic for given inputs.
+struct SegPair { int seq, tok0, tok1, lo, hi, jb, n; };
+
+__device__ __forceinline__ SegPair seg_pair(const Problem &p, int tpb, int nchunks, int z) {
+    SegPair s;
+    s.seq = z / nchunks;
+    s.tok0 = (z % nchunks) * tpb;
+    s.tok1 = min(p.T, s.tok0 + tpb);
+    s.lo = INT_MAX; s.hi = 0;
+    for (int t = s.tok0; t < s.tok1; t++) {
+        const int ps = tok_pos(p, s.seq, t);
+        s.lo = min(s.lo, win_lo(ps, p.window)); s.hi = max(s.hi, ps + 1);
+    }
+    s.jb = (s.lo / 16) * 16;
+    s.n = (s.hi - s.jb + 15) / 16;
+    return s;
+}
+
+// The same for a z that is equal in every lane of the wave (seg_pair itself also serves one pair per lane).
+__device__ __forceinline__ SegPair seg_pair_u(const Problem &p, int tpb, int nchunks, int z) {
+    SegPair s = seg_pair(p, tpb, nchunks, __builtin_amdgcn_readfirstlane(z));
+    s.lo = __builtin_amdgcn_readfirstlane(s.lo); s.hi = __builtin_amdgcn_readfirstlane(s.hi);
+    s.jb = __builtin_amdgcn_readfirstlane(s.jb); s.n = __builtin_amdgcn_readfirstlane(s.n);
+    return s;
+}
+
+// Over pairs z = 0 .. nseq * nchunks - 1 (pair z holds NKV * n_z tiles): the total N, the pair zx holding global
+// tile x and the tiles before it px, and the tiles before pair zq (pq). Called by whole waves (wave-uniform).
+__device__ __forceinline__ void seg_scan(const Problem &p, int tpb, int nchunks, int x, int zq, int &N, int &zx,
+                                         int &px, int &pq) {
+    const int lane = threadIdx.x & 63, nz = p.nseq * nchunks;
+    N = 0; zx = -1; px = 0; pq = 0;
+    for (int z0 = 0; z0 < nz; z0 += 64) {
+        const int zl = z0 + lane;
+        const int cnt = zl < nz ? p.NKV * seg_pair(p, tpb, nchunks, zl).n : 0;
+        int incl = cnt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
+        }
+        if (zq >= z0 && zq < z0 + 64) pq = N + __shfl(incl, zq - z0) - __shfl(cnt, zq - z0);
+        if (zx < 0) {
+            const unsigned long long hit = __ballot(N + incl > x);
+            if (hit) {
+                const int l = __builtin_ctzll(hit);
+                zx = z0 + l;
+                px = N + __shfl(incl, l) - __shfl(cnt, l);
+            }
+        }
+        N += __shfl(incl, 63);
+    }
+    // The results are the same in every lane: say so, so that they and what derives from them live in SGPRs.
+    N = __builtin_amdgcn_readfirstlane(N); zx = __builtin_amdgcn_readfirstlane(zx);
+    px = __builtin_amdgcn_readfirstlane(px); pq = __builtin_amdgcn_readfirstlane(pq);
+}
+
 // LSE combine of the chunk partials of one (row, head) by one wave. Lane c holds the statistics of chunk c (64
 // at a time); lane d holds 4 head dims. The partial accumulators of the first NB chunks are requested before
 // the statistics are reduced, so a row with up to NB chunks costs one memory round trip. Chunks are summed in
@@ -62,8 +127,18 @@ __device__ __forceinline__ void combine_wave(const Problem &p, const Partials &p
     constexpr int NB = 16;                           // partial rows in flight per lane (the chunks of 8K keys at 512)
     const int lane = threadIdx.x & 63;
     const int r = s * p.T + t;
-    const int pos = tok_pos(p, s, t), lo = win_lo(pos, p.window);
-    const int c_lo = lo / C, n = pos / C - c_lo + 1;
+    int c_lo, n;
+    if (part.seg_g > 0) {                            // verify_kernel's runs: slots 0 .. n-1 of the row's pair
+        const int z = s * part.seg_nchunks + t / part.seg_tpb, kvh = h / (p.NQ / p.NKV);
+        int N, zx, px, pz;
+        seg_scan(p, part.seg_tpb, part.seg_nchunks, INT_MAX, z, N, zx, px, pz);
+        const int q = max((N + part.seg_g - 1) / part.seg_g, part.seg_qmin);
+        const int nz = seg_pair_u(p, part.seg_tpb, part.seg_nchunks, z).n, S = pz + kvh * nz;
+        c_lo = 0; n = min((S + nz - 1) / q - S / q + 1, part.ns_cap);
+    } else {
+        const int pos = tok_pos(p, s, t), lo = win_lo(pos, p.window);
+        c_lo = lo / C; n = pos / C - c_lo + 1;
+    }
     const size_t base = ((size_t)r * p.NQ + h) * part.ns_cap + c_lo;
     const float *accb = part.acc + base * HD;
     f32x4 v[NB];
@@ -455,31 +530,23 @@ struct VerifyCfg {
     static_assert(NLD >= 1 && (KT * SLOTS) % (NW * 64) == 0, "tile loads");
 };
 
+// Tiles [t0, t1) of pair sp, KV head kvh (keys sp.jb + 16 t ..), into partial slot `slot`. Called by all waves;
+// returns with every load landed (the caller's barrier then frees the ring).
 template <int HD, int RB, int KVT, int QT>
-__global__ void __launch_bounds__(256) verify_kernel(const SplitArgs a) {
+__device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair &sp, int kvh, int t0, int t1, int slot,
+                                               unsigned char *smem) {
     using Cf = VerifyCfg<HD>;
     constexpr int NS = Cf::NS, KT = Cf::KT, KS = Cf::KS, DB = Cf::DB, NLD = Cf::NLD, SLOTS = Cf::SLOTS;
     constexpr int ROWB = Cf::ROWB;
     constexpr bool F16 = OpIsF16<KVT>::value;
     using KE = typename Elem<KVT>::T;
     using QE = typename Elem<QT>::T;
-    extern __shared__ __align__(16) unsigned char smem[];
-
     const Problem &p = a.p;
-    const int kvh = blockIdx.x, c = blockIdx.y;
-    const int seq = blockIdx.z / a.nchunks, tchunk = blockIdx.z % a.nchunks;
-    const int GRP = p.NQ / p.NKV;
-    const int tok0 = tchunk * a.tpb, tok1 = min(p.T, tok0 + a.tpb);
-    const int nrows = (tok1 - tok0) * GRP;
-    int lo_b = INT_MAX, hi_b = 0;
-    for (int t = tok0; t < tok1; t++) {
-        const int ps = tok_pos(p, seq, t);
-        lo_b = min(lo_b, win_lo(ps, p.window)); hi_b = max(hi_b, ps + 1);
-    }
-    const int C = a.C;
-    const int j_lo = max(c * C, lo_b), j_hi = min(c * C + C, hi_b);
-    if (j_lo >= j_hi) return;
-
+    const int GRP = p.NQ / p.NKV, seq = sp.seq, tok0 = sp.tok0, tok1 = sp.tok1;
+    const int nrows = (tok1 - tok0) * GRP, lo_b = sp.lo, hi_b = sp.hi;
+    (void)lo_b;
+    const int jb = sp.jb + KT * t0, ntile = t1 - t0;
+    const int j_lo = max(jb, sp.lo), j_hi = min(sp.jb + KT * t1, sp.hi);
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, ln = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool active = wave < RB;
@@ -510,8 +577,6 @@ __global__ void __launch_bounds__(256) verify_kernel(const SplitArgs a) {
     // Tile k (keys jb + KT k ..) -> stage k % NS. Thread slot S of a tensor's tile holds the 16-byte column
     // (S % SLOTS) ^ vswz(key) of key row S / SLOTS; keys past the end re-read the last key (they are masked)
     // and tiles past the last re-read the last.
-    const int jb = (j_lo / KT) * KT;
-    const int ntile = (j_hi - jb + KT - 1) / KT;
     auto issue = [&](int k) {
         const int jt = min(jb + KT * k, ((hi_b - 1) / KT) * KT), jrow = key_row(p, jt);
         unsigned char *kd = smem + (size_t)(k % NS) * Cf::STAGE, *vd = kd + Cf::TILE;
@@ -519,8 +584,8 @@ __global__ void __launch_bounds__(256) verify_kernel(const SplitArgs a) {
         for (int u = 0; u < NLD; u++) {
             const int i = wave * NLD + u, S = i * 64 + lane, key = S / SLOTS;
             const size_t off = (size_t)(jrow + min(key, hi_b - 1 - jt)) * krow + (size_t)(((S % SLOTS) ^ vswz(key)) * 8);
-            __builtin_amdgcn_global_load_lds((vglb_void *)(Kb + off), (vlds_void *)(kd + (size_t)i * 1024), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((vglb_void *)(Vb + off), (vlds_void *)(vd + (size_t)i * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((vglb_void *)(Kb + off), (vlds_void *)(kd + (size_t)i * 1024), 16, 0, 2);
+            __builtin_amdgcn_global_load_lds((vglb_void *)(Vb + off), (vlds_void *)(vd + (size_t)i * 1024), 16, 0, 2);
         }
     };
     // Tiles past the last are issued too (stages never read), so every wait sees the same count.
@@ -542,7 +607,7 @@ __global__ void __launch_bounds__(256) verify_kernel(const SplitArgs a) {
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD * (NS - 2)) : "memory");
         __syncthreads();
         issue(it + NS - 1);
-        if (!active) continue;
+        // waves past the last row block compute too (their rows are masked): a branch here costs registers
         const int jt = jb + KT * it;
         const unsigned stage = (it % NS) * Cf::STAGE;
         unsigned kb = kaddr + stage, vb = vaddr + stage;
@@ -597,10 +662,39 @@ __global__ void __launch_bounds__(256) verify_kernel(const SplitArgs a) {
     l = sum_over_groups(l);
     if (!valid) return;
     const int r = seq * p.T + tq, h = kvh * GRP + rho % GRP;
-    const size_t pi = ((size_t)r * p.NQ + h) * a.part.ns_cap + c;
+    const size_t pi = ((size_t)r * p.NQ + h) * a.part.ns_cap + slot;
 #pragma unroll
     for (int db = 0; db < DB; db++) *reinterpret_cast<f32x4 *>(a.part.acc + pi * HD + 16 * db + 4 * g) = acc[db];
     if (g == 0) { a.part.m[pi] = m; a.part.l[pi] = l; }
+}
+
+template <int HD, int RB, int KVT, int QT>
+__global__ void __launch_bounds__(256) verify_kernel(const SplitArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const Problem &p = a.p;
+    const int w = blockIdx.x, G = gridDim.x;
+    int N, z, P, pz;
+    seg_scan(p, a.tpb, a.nchunks, INT_MAX, 0, N, z, P, pz);
+    const int q = max((N + G - 1) / G, a.part.seg_qmin);
+    const long long xs = (long long)w * q;
+    if (xs >= N) return;
+    int x = (int)xs;
+    const int x1 = (int)min((long long)N, xs + q);
+    seg_scan(p, a.tpb, a.nchunks, x, 0, N, z, P, pz);
+    SegPair sp = seg_pair_u(p, a.tpb, a.nchunks, z);
+    for (;;) {
+        const int local = x - P, kvh = local / sp.n, t0 = local % sp.n;
+        const int t1 = min(sp.n, t0 + (x1 - x)), slot = w - (P + kvh * sp.n) / q;
+        if (kvh >= p.NKV || slot < 0 || slot >= a.part.ns_cap) break;   // unreachable while the counts agree
+        verify_segment<HD, RB, KVT, QT>(a, sp, kvh, t0, t1, slot, smem);
+        x += t1 - t0;
+        if (x >= x1) break;
+        if (t1 == sp.n && kvh == p.NKV - 1) {            // next pair (every pair holds at least one tile)
+            P += p.NKV * sp.n;
+            sp = seg_pair_u(p, a.tpb, a.nchunks, ++z);
+        }
+        __syncthreads();                                 // every wave is done with the ring
+    }
 }
 
 // LSE combine: one wave per (row, head).
@@ -614,19 +708,53 @@ __global__ void __launch_bounds__(kCombineWaves * 64) combine_kernel(const Probl
 }
 
 // ---------------------------------------------------------------- host side
+// verify_kernel's grid: the workgroups that are resident at once on the current device (per device, cached).
 template <int HD, int RB, int KVT, int QT>
-static hipError_t launch_split_t(const SplitArgs &a, dim3 grid, hipStream_t st) {
+static hipError_t verify_grid(int &G) {
+    using Cf = VerifyCfg<HD>;
+    static int per_cu = 0;
+    static int ncu[64] = {0};
+    if (per_cu == 0) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&verify_kernel<HD, RB, KVT, QT>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cf::LDS);
+        if (e != hipSuccess) return e;
+        int nb = 0;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void *>(&verify_kernel<HD, RB, KVT, QT>),
+                                                         256, Cf::LDS);
+        if (e != hipSuccess) return e;
+        per_cu = nb > 0 ? nb : 1;
+    }
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (ncu[dev] == 0) {
+        int n = 0;
+        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        ncu[dev] = n > 0 ? n : 1;
+    }
+    G = per_cu * ncu[dev];
+    return hipSuccess;
+}
+
+template <int HD, int RB, int KVT, int QT>
+static hipError_t launch_split_t(SplitArgs &a, dim3 grid, hipStream_t st) {
     if constexpr (RB >= 2 && HD <= 256 && KVT != DT_FP32) {
-        using Cf = VerifyCfg<HD>;
-        static bool configured_v = false;
-        if (!configured_v) {
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&verify_kernel<HD, RB, KVT, QT>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cf::LDS);
+        if (a.part.ns_cap >= 2) {
+            int G = 0;
+            hipError_t e = verify_grid<HD, RB, KVT, QT>(G);
             if (e != hipSuccess) return e;
-            configured_v = true;
+            // q >= qmin keeps a pair within ns_cap slots: a pair of n <= max_pos/16 + 1 tiles meets at most
+            // floor((n - 1) / q) + 2 runs.
+            const int nmax = a.p.max_pos / 16 + 1;
+            a.part.seg_g = G;
+            a.part.seg_qmin = std::max(8, (nmax - 1) / (a.part.ns_cap - 1) + 1);
+            a.part.seg_tpb = a.tpb;
+            a.part.seg_nchunks = a.nchunks;
+            hipLaunchKernelGGL((verify_kernel<HD, RB, KVT, QT>), dim3(G), dim3(256), VerifyCfg<HD>::LDS, st, a);
+            return hipGetLastError();
         }
-        hipLaunchKernelGGL((verify_kernel<HD, RB, KVT, QT>), grid, dim3(256), Cf::LDS, st, a);
-        return hipGetLastError();
     }
     using Cf = SplitCfg<HD, RB>;
     static bool configured = false;
@@ -641,7 +769,7 @@ static hipError_t launch_split_t(const SplitArgs &a, dim3 grid, hipStream_t st) 
 }
 
 template <int HD, int KVT, int QT>
-static hipError_t dispatch_rb(const SplitArgs &a, int RB, dim3 grid, hipStream_t st) {
+static hipError_t dispatch_rb(SplitArgs &a, int RB, dim3 grid, hipStream_t st) {
     switch (RB) {
     case 1: return launch_split_t<HD, 1, KVT, QT>(a, grid, st);
     case 2: return launch_split_t<HD, 2, KVT, QT>(a, grid, st);
@@ -652,7 +780,7 @@ static hipError_t dispatch_rb(const SplitArgs &a, int RB, dim3 grid, hipStream_t
 }
 
 template <int KVT, int QT>
-static hipError_t dispatch_hd(const SplitArgs &a, int RB, dim3 grid, hipStream_t st) {
+static hipError_t dispatch_hd(SplitArgs &a, int RB, dim3 grid, hipStream_t st) {
     switch (a.p.HD) {
     case 128: return dispatch_rb<128, KVT, QT>(a, RB, grid, st);
     case 512: return dispatch_rb<512, KVT, QT>(a, RB, grid, st);
@@ -677,7 +805,8 @@ size_t partial_rows(const Problem &p, int chunk) {
     return (size_t)p.nseq * p.T * p.NQ * (size_t)(p.max_pos / chunk + 1);
 }
 
-hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipStream_t st) {
+hipError_t launch_split(const Problem &p, int chunk, Partials &part, hipStream_t st) {
+    part.seg_g = 0;
     if (chunk <= 0 || chunk % 16) return hipErrorInvalidValue;
     // Up to 16 rows per KV head (one query token at GRP <= 16): the streaming decode kernel.
     if (decode_stream_supported(p))
@@ -691,13 +820,16 @@ hipError_t launch_split(const Problem &p, int chunk, const Partials &part, hipSt
     SplitArgs a{p, part, chunk, tpb, nchunks, p.scale * kLog2e};
     dim3 grid(p.NKV, p.max_pos / chunk + 1, p.nseq * nchunks);
     if (grid.z > 65535u || grid.y > 65535u) return hipErrorInvalidConfiguration;
+    if ((long long)p.nseq * p.NKV * (p.max_pos / 16 + 2) > INT_MAX) return hipErrorInvalidConfiguration;
     const int kv = p.kv_dtype, q = p.q_dtype;
-    if (kv == DT_F16 && q == DT_FP32) return dispatch_hd<DT_F16, DT_FP32>(a, RB, grid, st);
-    if (kv == DT_F16 && q == DT_F16) return dispatch_hd<DT_F16, DT_F16>(a, RB, grid, st);
-    if (kv == DT_BF16 && q == DT_FP32) return dispatch_hd<DT_BF16, DT_FP32>(a, RB, grid, st);
-    if (kv == DT_BF16 && q == DT_BF16) return dispatch_hd<DT_BF16, DT_BF16>(a, RB, grid, st);
-    if (kv == DT_FP32 && q == DT_FP32) return dispatch_hd<DT_FP32, DT_FP32>(a, RB, grid, st);
-    return hipErrorInvalidValue;
+    hipError_t e = hipErrorInvalidValue;
+    if (kv == DT_F16 && q == DT_FP32) e = dispatch_hd<DT_F16, DT_FP32>(a, RB, grid, st);
+    else if (kv == DT_F16 && q == DT_F16) e = dispatch_hd<DT_F16, DT_F16>(a, RB, grid, st);
+    else if (kv == DT_BF16 && q == DT_FP32) e = dispatch_hd<DT_BF16, DT_FP32>(a, RB, grid, st);
+    else if (kv == DT_BF16 && q == DT_BF16) e = dispatch_hd<DT_BF16, DT_BF16>(a, RB, grid, st);
+    else if (kv == DT_FP32 && q == DT_FP32) e = dispatch_hd<DT_FP32, DT_FP32>(a, RB, grid, st);
+    part = a.part;                                     // the combine reads how the partials were laid out
+    return e;
 }
 
 hipError_t launch_combine(const Problem &p, int chunk, const Partials &part, hipStream_t st) {
