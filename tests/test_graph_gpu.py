@@ -1,0 +1,91 @@
+"""HIP graph capture of the attention launches (the reference's Gemma decode captures its attention launches into a
+graph, models/gemma4_decode_graph.cuh; the scratch is reserved before capture and launches never allocate,
+models/gemma4_decode.cu:318).
+
+Positions are read on the device and the decode / verify grids are sized by max_pos (or by the resident
+workgroups), so one graph captured at the cache capacity serves every later step: the position buffers are
+rewritten in place between replays. Each replay must equal an eager call on the same inputs bit for bit, with
+eager work and synchronisations between the replays.
+"""
+import numpy as np
+import pytest
+import torch
+
+import dgx_attn as A
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _cache(seed, B, ML, NKV, HD):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return (torch.randn(B, ML, NKV, HD, device="cuda", generator=g) * 0.5).half()
+
+
+def test_decode_graph_replays_with_new_positions():
+    B, NQ, NKV, HD, ML = 6, 24, 4, 256, 2048
+    K, V = _cache(1, B, ML, NKV, HD), _cache(2, B, ML, NKV, HD)
+    Q = torch.randn(B * NQ * HD, device="cuda").half()
+    pos = torch.full((B,), 100, dtype=torch.int32, device="cuda")
+    Og = torch.empty_like(Q); Oe = torch.empty_like(Q)
+    stride = ML * NKV * HD
+    A.split_reserve(B, NQ, ML, HD)
+    A.attn_batch(Q, K, V, Og, B, 1, NQ, NKV, HD, pos, stride, ML - 1)        # eager first call (warm-up)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        A.attn_batch(Q, K, V, Og, B, 1, NQ, NKV, HD, pos, stride, ML - 1)
+    rng = np.random.default_rng(7)
+    for step in range(4):
+        p = rng.integers(0, ML, size=B).astype(np.int32)
+        pos.copy_(torch.from_numpy(p).cuda())
+        g.replay()
+        A.attn_batch(Q, K, V, Oe, B, 1, NQ, NKV, HD, pos, stride, ML - 1)
+        torch.cuda.synchronize()
+        assert torch.equal(Og.view(torch.int16), Oe.view(torch.int16)), f"replay {step} positions {p.tolist()}"
+
+
+def test_tree_verify_graph_replays_with_new_bases():
+    B, NQ, NKV, HD, Tq, ML = 4, 24, 4, 256, 8, 4096
+    K, V = _cache(3, B, ML, NKV, HD), _cache(4, B, ML, NKV, HD)
+    Q = torch.randn(B * Tq * NQ * HD, device="cuda").half()
+    anc = np.stack([oracle.tree_anc(oracle.tree_random(50 + b, Tq, 2, 7)[0]) for b in range(B)]).astype(np.uint32)
+    ancd = torch.from_numpy(anc.reshape(-1).view(np.int32)).cuda()
+    base_b = torch.full((B,), 64, dtype=torch.int32, device="cuda")
+    max_pos = ML - 1
+    Og = torch.empty_like(Q); Oe = torch.empty_like(Q)
+    stride = ML * NKV * HD
+    A.split_reserve(B * Tq, NQ, ML, HD)
+    A.attn_batch(Q, K, V, Og, B, Tq, NQ, NKV, HD, base_b, stride, max_pos, chunk=512, anc=ancd)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        A.attn_batch(Q, K, V, Og, B, Tq, NQ, NKV, HD, base_b, stride, max_pos, chunk=512, anc=ancd)
+    rng = np.random.default_rng(8)
+    for step in range(4):
+        b = rng.integers(0, ML - Tq + 1, size=B).astype(np.int32)
+        base_b.copy_(torch.from_numpy(b).cuda())
+        g.replay()
+        A.attn_batch(Q, K, V, Oe, B, Tq, NQ, NKV, HD, base_b, stride, max_pos, chunk=512, anc=ancd)
+        torch.cuda.synchronize()
+        assert torch.equal(Og.view(torch.int16), Oe.view(torch.int16)), f"replay {step} bases {b.tolist()}"
+
+
+def test_prefill_graph_replays_with_new_queries():
+    T, NQ, NKV, HD = 256, 16, 8, 256
+    g0 = torch.Generator(device="cuda").manual_seed(5)
+    K = torch.randn(T, NKV, HD, device="cuda", generator=g0).bfloat16()
+    V = torch.randn(T, NKV, HD, device="cuda", generator=g0).bfloat16()
+    Q = torch.randn(T * NQ * HD, device="cuda", generator=g0).bfloat16()
+    Og = torch.empty_like(Q); Oe = torch.empty_like(Q)
+    A.attn_prefill(Q, K, V, Og, 1, T, NQ, NKV, HD)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        A.attn_prefill(Q, K, V, Og, 1, T, NQ, NKV, HD)
+    for step in range(3):
+        Q.copy_(torch.randn(T * NQ * HD, device="cuda", generator=g0).bfloat16())
+        g.replay()
+        A.attn_prefill(Q, K, V, Oe, 1, T, NQ, NKV, HD)
+        torch.cuda.synchronize()
+        assert torch.equal(Og.view(torch.int16), Oe.view(torch.int16)), f"replay {step}"
