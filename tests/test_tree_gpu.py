@@ -80,3 +80,33 @@ def test_config5_batched_tree_verify(tree):
                                tree_base=np.repeat(base_b, Tq))
     assert_close(O.cpu().numpy().reshape(B * Tq, NQ, HD), ref, f"config5 {tree}", lse.cpu().numpy().reshape(-1, NQ),
                  ref_lse)
+
+
+@pytest.mark.parametrize("kvdt", [1, 2])
+@pytest.mark.parametrize("HD,NQ,NKV,Tq", [(128, 16, 2, 12), (128, 32, 4, 9), (256, 16, 4, 20)])
+def test_ragged_tree_verify_shapes(kvdt, HD, NQ, NKV, Tq):
+    """Tree verify at HD 128 and with more than 64 query rows per KV head (several token tiles per sequence), ragged
+    committed lengths that are not multiples of the 16-key tile, f16 and bf16 caches, against the oracle."""
+    B = 5
+    committed = oracle.gen_uniform_int(71 + HD + Tq, 1, 3000, B)
+    parents = [oracle.tree_random(300 + b, Tq, 3, 6)[0] for b in range(B)]
+    anc = np.stack([oracle.tree_anc(p) for p in parents]).astype(np.uint32)
+    ML = 3000 + Tq
+    lens = committed + Tq
+    kv, kd = normal_cache(81 + HD, B, ML, NKV, HD, lens, 0.5, kvdt)
+    vv, vd = normal_cache(82 + HD, B, ML, NKV, HD, lens, 0.5, kvdt)
+    q = oracle.gen_normal(83 + HD, B * Tq * NQ * HD)
+    base_b = committed.astype(np.int32)
+    max_pos = int((base_b + Tq - 1).max())
+    A.split_reserve(B * Tq, NQ, max_pos + 1, HD)
+    O = torch.empty(B * Tq * NQ * HD, device="cuda"); lse = torch.empty(B * Tq * NQ, device="cuda")
+    A.attn_batch(dev(q), kd, vd, O, B, Tq, NQ, NKV, HD, dev(base_b), ML * NKV * HD, max_pos, chunk=512,
+                 anc=dev(anc.reshape(-1).view(np.int32)), lse=lse)
+    torch.cuda.synchronize()
+    pos = (base_b[:, None] + np.arange(Tq)[None, :]).reshape(-1)
+    kv_off = np.repeat(np.arange(B, dtype=np.int64) * ML * NKV * HD, Tq)
+    qr, _ = oracle.round_to(q, kvdt)        # the kernel feeds Q to the MFMA in the cache's 16-bit type
+    ref, ref_lse = oracle_rows(qr, kv, vv, kv_off, pos, NQ, NKV, HD, anc=anc.reshape(-1),
+                               tree_base=np.repeat(base_b, Tq))
+    assert_close(O.cpu().numpy().reshape(B * Tq, NQ, HD), ref, f"tree HD{HD} Tq{Tq} kv{kvdt}",
+                 lse.cpu().numpy().reshape(-1, NQ), ref_lse)
