@@ -25,7 +25,7 @@ def _ring_of(lin, last, cap):
 
 
 @pytest.mark.parametrize("kvdt", [1, 2])
-@pytest.mark.parametrize("Tq,cap", [(1, 1088), (3, 1088), (1, 1024)])
+@pytest.mark.parametrize("Tq,cap", [(1, 1088), (3, 1088), (1, 1024), (12, 1088)])
 def test_ring_decode_equals_linear(kvdt, Tq, cap):
     """cap = window: the ring is exactly full, and the tile holding a row's first key also reads ring rows that
     hold newer keys (masked)."""
