@@ -352,6 +352,18 @@ static hipError_t dec_dispatch_hd(const DecodeArgs &a, dim3 grid, int rw, hipStr
     }
 }
 
+// Upper bound of the work items (sequence, chunk, kv head) of a launch: every chunk up to max_pos, or, under a sliding
+// window with consecutive token positions, the at most (window + T - 2) / chunk + 2 chunks a window of window + T - 1
+// keys meets (a 32K-key cache with a 1K window then launches 6 items per sequence and head, not 128).
+static long long decode_items_bound(const Problem &p, int chunk) {
+    long long per = p.max_pos / chunk + 1;
+    if (p.window > 0 && (p.T == 1 || p.pos_mode == 1)) {
+        const long long w = ((long long)p.window + p.T - 2) / chunk + 2;
+        if (w < per) per = w;
+    }
+    return per * p.NKV * p.nseq;
+}
+
 bool decode_stream_supported(const Problem &p) {
     // One 16-row block (RW = 1). The kernel also runs RW = 2..4 row blocks, one wave each per key lane, but then
     // the row waves re-read every tile, which measured slower than the cooperative split kernel on the B=16 x
@@ -365,7 +377,7 @@ hipError_t launch_decode_stream(const Problem &p, int chunk, const Partials &par
     if (chunk <= 0 || chunk % 16) return hipErrorInvalidValue;
     if (p.max_pos / chunk + 1 > part.ns_cap) return hipErrorInvalidValue;
     DecodeArgs a{p, part, chunk, p.scale * kLog2e};
-    const long long items = (long long)p.NKV * (p.max_pos / chunk + 1) * p.nseq;   // upper bound of the work items
+    const long long items = decode_items_bound(p, chunk);
     if (items > INT_MAX) return hipErrorInvalidConfiguration;
     dim3 grid((unsigned)items);
     const int rw = (p.T * (p.NQ / p.NKV) + 15) / 16;   // 16-row blocks, one wave each per key lane
@@ -575,7 +587,7 @@ hipError_t launch_decode_f32(const Problem &p, int chunk, const Partials &part, 
     if (chunk <= 0 || chunk % 16) return hipErrorInvalidValue;
     if (p.max_pos / chunk + 1 > part.ns_cap) return hipErrorInvalidValue;
     DecodeArgs a{p, part, chunk, p.scale * kLog2e};
-    const long long items = (long long)p.NKV * (p.max_pos / chunk + 1) * p.nseq;
+    const long long items = decode_items_bound(p, chunk);
     if (items > INT_MAX) return hipErrorInvalidConfiguration;
     dim3 grid((unsigned)items);
     if (p.HD == 128) {
