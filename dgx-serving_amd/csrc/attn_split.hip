@@ -576,9 +576,9 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
 
     // Tile k (keys jb + KT k ..) -> stage k % NS. Thread slot S of a tensor's tile holds the 16-byte column
     // (S % SLOTS) ^ vswz(key) of key row S / SLOTS; keys past the end re-read the last key (they are masked)
-    // and tiles past the last re-read the last.
+    // and tiles past the segment's last re-read that tile (an L2 hit, not the next run's keys).
     auto issue = [&](int k) {
-        const int jt = min(jb + KT * k, ((hi_b - 1) / KT) * KT), jrow = key_row(p, jt);
+        const int jt = jb + KT * min(k, ntile - 1), jrow = key_row(p, jt);
         unsigned char *kd = smem + (size_t)(k % NS) * Cf::STAGE, *vd = kd + Cf::TILE;
 #pragma unroll
         for (int u = 0; u < NLD; u++) {
