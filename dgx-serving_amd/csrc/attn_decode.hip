@@ -155,27 +155,28 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
     const int k1 = r_lo >= r_hi ? k0 : (tb1 < kl ? 0 : (tb1 - kl) / NKL + 1);
     // Loads of tile k (K straight into A fragments; V rows coalesced for the private LDS transpose).
     // With RW > 1 the RW waves of a key lane read the same tiles: plain loads, so the L2 serves the repeats.
-    auto load = [&](int k, u32x4 (&kf)[Cf::VCH], u32x4 (&vr)[Cf::VCH]) {
+    // which: 1 = K, 2 = V, 3 = both.
+    auto load_t = [&](int k, u32x4 (&kf)[Cf::VCH], u32x4 (&vr)[Cf::VCH], int which) {
         const int jt = c * C + KT * (kl + NKL * k), jrow = key_row(p, jt);
 #pragma unroll
         for (int u = 0; u < Cf::VCH; u++) {      // whole rows, 16 bytes per lane; the last tile clamps to the last key
             const int q = lane + 64 * u, key = q / (HD / 8), col = (q % (HD / 8)) * 8;
             const size_t off = (size_t)(jrow + min(key, hi - 1 - jt)) * krow + col;
             if constexpr (RW == 1) {
-                kf[u] = load8_op_stream<KVT, F16>(Kb + off);
-                vr[u] = load8_op_stream<KVT, F16>(Vb + off);
+                if (which & 1) kf[u] = load8_op_stream<KVT, F16>(Kb + off);
+                if (which & 2) vr[u] = load8_op_stream<KVT, F16>(Vb + off);
             } else {
-                kf[u] = load8_op<KVT, F16>(Kb + off);
-                vr[u] = load8_op<KVT, F16>(Vb + off);
+                if (which & 1) kf[u] = load8_op<KVT, F16>(Kb + off);
+                if (which & 2) vr[u] = load8_op<KVT, F16>(Vb + off);
             }
         }
     };
-    // PF + 1 register buffers: the loads of tiles k + 1 .. k + PF are in flight while tile k is computed (PF = 0:
-    // load, then compute; measured fastest on the B=16 ragged workload, where the lower register count lets every
-    // chunk's workgroup be resident at once). The first PF tiles are requested before the Q rows are staged.
-    constexpr int PF = 0, NBUF = PF + 1;
-    u32x4 kb[NBUF][Cf::VCH], vb[NBUF][Cf::VCH];
-    static_for<PF>([&](auto i) { if (k0 + i < k1) load(k0 + i, kb[i], vb[i]); });
+    auto load = [&](int k, u32x4 (&kf)[Cf::VCH], u32x4 (&vr)[Cf::VCH]) { load_t(k, kf, vr, 3); };
+    // One register buffer per tensor. Tile k's K (V) registers are refilled with tile k+1's as soon as they have
+    // gone to LDS, so the next tile's loads fly while tile k is computed; tile k0 is requested before the Q rows
+    // are staged.
+    u32x4 kb[Cf::VCH], vb[Cf::VCH];
+    if (k0 < k1) load(k0, kb, vb);
 #pragma unroll
     for (int u = 0; u < QCH; u++) *reinterpret_cast<u32x4 *>(qs + qrow_of(u) * Cf::QSTR + qcol_of(u)) = qv[u];
     RowMask rm;
@@ -193,8 +194,9 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
 #pragma unroll
     for (int db = 0; db < Cf::DB; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     const uint16_t *qrow = qs + (r_lo + ln) * Cf::QSTR + 8 * g;
-    auto compute = [&](int k, const u32x4 (&kr)[Cf::VCH], const u32x4 (&vr)[Cf::VCH]) {
+    auto compute = [&](int k, u32x4 (&kr)[Cf::VCH], u32x4 (&vr)[Cf::VCH]) {
         const int jt = c * C + KT * (kl + NKL * k);
+        const bool more = k + 1 < k1;
         // K rows through the wave's LDS slice into MFMA A fragments (lane = key ln, 16 bytes of dims 32 ks + 8 g).
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -203,6 +205,7 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
             *reinterpret_cast<u32x4 *>(kls + key * Cf::VSTR + col) = kr[u];
         }
         __builtin_amdgcn_wave_barrier();
+        if (more) load_t(k + 1, kr, vr, 1);
         // S^T[key jt + 4g + i][row ln], two independent MFMA chains.
         f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
 #pragma unroll
@@ -249,18 +252,12 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
             *reinterpret_cast<u32x4 *>(vs + key * Cf::VSTR + col) = vr[u];
         }
         __builtin_amdgcn_wave_barrier();
+        if (more) load_t(k + 1, kr, vr, 2);
         const uint16_t *vt = vs + (4 * g + (ln >> 2)) * Cf::VSTR + 4 * (ln & 3);
 #pragma unroll
         for (int db = 0; db < Cf::DB; db++) acc[db] = mfma16k16<F16>(lds_read_tr16(vt + 16 * db), pop, acc[db]);
     };
-    for (int k = k0; k < k1; k += NBUF) {
-        static_for<NBUF>([&](auto j) {
-            const int kk = k + j;
-            if (kk >= k1) return;
-            if (kk + PF < k1) load(kk + PF, kb[(j + PF) % NBUF], vb[(j + PF) % NBUF]);
-            compute(kk, kb[j], vb[j]);
-        });
-    }
+    for (int k = k0; k < k1; k++) compute(k, kb, vb);
     l = sum_over_groups(l);
 #ifdef DGX_TRACE
     if (lane == 0) {
