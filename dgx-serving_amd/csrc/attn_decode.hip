@@ -90,7 +90,7 @@ __device__ __forceinline__ bool find_item(const Problem &p, int C, int &seq, int
     return false;
 }
 
-template <int HD, int NKL_, int RW_, int KVT, int QT>
+template <int HD, int NKL_, int RW_, int KVT, int QT, bool EARLY>
 __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const DecodeArgs a) {
 #ifdef DGX_TRACE
     const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
@@ -172,11 +172,12 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
         }
     };
     auto load = [&](int k, u32x4 (&kf)[Cf::VCH], u32x4 (&vr)[Cf::VCH]) { load_t(k, kf, vr, 3); };
-    // One register buffer per tensor. Tile k's K (V) registers are refilled with tile k+1's as soon as they have
-    // gone to LDS, so the next tile's loads fly while tile k is computed; tile k0 is requested before the Q rows
-    // are staged.
+    // One register buffer per tensor. EARLY: tile k's K (V) registers are refilled with tile k+1's as soon as they
+    // have gone to LDS, so the next tile's loads fly while tile k is computed, and tile k0 is requested before the
+    // Q rows are staged (the sliding-window case, few waves per SIMD). Otherwise load, then compute (config 2: two
+    // waves per SIMD already overlap one's loads with the other's math, and this measured 0.5% faster there).
     u32x4 kb[Cf::VCH], vb[Cf::VCH];
-    if (k0 < k1) load(k0, kb, vb);
+    if (EARLY && k0 < k1) load(k0, kb, vb);
 #pragma unroll
     for (int u = 0; u < QCH; u++) *reinterpret_cast<u32x4 *>(qs + qrow_of(u) * Cf::QSTR + qcol_of(u)) = qv[u];
     RowMask rm;
@@ -196,7 +197,7 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
     const uint16_t *qrow = qs + (r_lo + ln) * Cf::QSTR + 8 * g;
     auto compute = [&](int k, u32x4 (&kr)[Cf::VCH], u32x4 (&vr)[Cf::VCH]) {
         const int jt = c * C + KT * (kl + NKL * k);
-        const bool more = k + 1 < k1;
+        const bool more = EARLY && k + 1 < k1;
         // K rows through the wave's LDS slice into MFMA A fragments (lane = key ln, 16 bytes of dims 32 ks + 8 g).
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -257,7 +258,10 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
 #pragma unroll
         for (int db = 0; db < Cf::DB; db++) acc[db] = mfma16k16<F16>(lds_read_tr16(vt + 16 * db), pop, acc[db]);
     };
-    for (int k = k0; k < k1; k++) compute(k, kb, vb);
+    for (int k = k0; k < k1; k++) {
+        if (!EARLY) load(k, kb, vb);
+        compute(k, kb, vb);
+    }
     l = sum_over_groups(l);
 #ifdef DGX_TRACE
     if (lane == 0) {
@@ -317,19 +321,25 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
     }
 }
 
-template <int HD, int RW, int KVT, int QT>
-static hipError_t launch_dec_rw(const DecodeArgs &a, dim3 grid, hipStream_t st) {
+template <int HD, int RW, int KVT, int QT, bool EARLY>
+static hipError_t launch_dec_e(const DecodeArgs &a, dim3 grid, hipStream_t st) {
     constexpr int NKL = 2;
     using Cf = DecodeCfg<HD, NKL, RW>;
     static bool configured = false;
     if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_stream_kernel<HD, NKL, RW, KVT, QT>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_stream_kernel<HD, NKL, RW, KVT, QT, EARLY>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cf::LDS);
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL((decode_stream_kernel<HD, NKL, RW, KVT, QT>), grid, dim3(Cf::NW * 64), Cf::LDS, st, a);
+    hipLaunchKernelGGL((decode_stream_kernel<HD, NKL, RW, KVT, QT, EARLY>), grid, dim3(Cf::NW * 64), Cf::LDS, st, a);
     return hipGetLastError();
+}
+template <int HD, int RW, int KVT, int QT>
+static hipError_t launch_dec_rw(const DecodeArgs &a, dim3 grid, hipStream_t st) {
+    // (the choice depends on the layer only, so a row's bits do not depend on the batch)
+    if (a.p.window > 0) return launch_dec_e<HD, RW, KVT, QT, true>(a, grid, st);
+    return launch_dec_e<HD, RW, KVT, QT, false>(a, grid, st);
 }
 
 template <int HD, int KVT, int QT>
