@@ -433,19 +433,20 @@ hipError_t dgx_attn_prefill_ex(const void *Q, int q_dtype, const void *Kc, const
                                int window, int kv_cap) {
     if (nseq == 0 || Sq == 0) return hipSuccess;
     if (!Q || !Kc || !Vc || !O || nseq < 0 || Sq < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || !valid_hd(HD) ||
-        max_pos < 0 || !valid_dtype(q_dtype) || !valid_dtype(o_dtype) || !valid_dtype(kv_dtype) || kv_split < 0 ||
-        kv_split % 64 || !ring_ok(kv_cap, window, Sq))
+        max_pos < 0 || !valid_dtype(q_dtype) || !valid_dtype(o_dtype) || !valid_dtype(kv_dtype) || kv_split < -1 ||
+        (kv_split > 0 && kv_split % 64) || !ring_ok(kv_cap, window, Sq))
         return hipErrorInvalidValue;
     Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
+    Problem p = make_problem(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, nseq, Sq, NQ, NKV, HD, kv_stride, 1,
+                             base, 1, base_b, nullptr, max_pos, scale, window);
+    p.kv_cap = kv_cap;
+    if (kv_split < 0) kv_split = prefill_auto_split(p);
     const int ns = kv_split > 0 ? max_pos / kv_split + 1 : 1;
     if (kv_split > 0) {
         std::lock_guard<std::mutex> lock(g_pool_mu);
         e = pool_grow(*pool, (size_t)nseq * Sq * NQ * ns, (size_t)HD);
         if (e != hipSuccess) return e;
     }
-    Problem p = make_problem(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, nseq, Sq, NQ, NKV, HD, kv_stride, 1,
-                             base, 1, base_b, nullptr, max_pos, scale, window);
-    p.kv_cap = kv_cap;
     Partials part{pool->m, pool->l, pool->acc, ns};
     return timed_launch(st, [&] { return launch_prefill(p, kv_split, part, st); });
 }

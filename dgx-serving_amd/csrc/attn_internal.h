@@ -78,6 +78,8 @@ hipError_t launch_decode_f32(const Problem &p, int chunk, const Partials &part, 
 // Flash prefill kernel (waves split query rows, K/V tiles shared through LDS). kv_split = 0: one pass per row
 // tile writing O directly; kv_split > 0: keys cut at absolute multiples of kv_split, partials + combine.
 hipError_t launch_prefill(const Problem &p, int kv_split, const Partials &part, hipStream_t st);
+// The key split chosen for kv_split = -1 (0: none).
+int prefill_auto_split(const Problem &p);
 // LSE combine of split partials for every (row, head).
 hipError_t launch_combine(const Problem &p, int chunk, const Partials &part, hipStream_t st);
 // Scratch requirement (rows*NQ*ns_cap) of a problem at a given chunk.

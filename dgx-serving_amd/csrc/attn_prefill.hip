@@ -466,6 +466,25 @@ static int pref_half_rows(int HD) {
     }
 }
 
+// Key split for kv_split = -1: when the unsplit grid would fill at most half of the CUs (a short run of queries
+// over a long cached prefix), cut the keys into as many absolute splits as whole grids fit on the CUs.
+int prefill_auto_split(const Problem &p) {
+    if (p.NQ % p.NKV) return 0;
+    const int GRP = p.NQ / p.NKV, HR = pref_half_rows(p.HD);
+    if (HR == 0 || GRP > HR) return 0;
+    const int tqh = HR / GRP, nht = (p.T + tqh - 1) / tqh;
+    const long nwg = (long)p.nseq * p.NKV * ((nht + 1) / 2);
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    if (nwg <= 0 || 2 * nwg > ncu) return 0;
+    const int nsplit = (int)(ncu / nwg);
+    const int keys = p.max_pos + 1;
+    int ks = (keys + nsplit - 1) / nsplit;
+    ks = ((ks + 63) / 64) * 64;
+    return ks >= keys ? 0 : ks;
+}
+
 hipError_t launch_prefill(const Problem &p, int kv_split, const Partials &part, hipStream_t st) {
     if (p.NQ % p.NKV || p.anc || p.pos_mode != 1) return hipErrorInvalidValue;
     const int GRP = p.NQ / p.NKV, HR = pref_half_rows(p.HD);

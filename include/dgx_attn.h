@@ -140,8 +140,10 @@ hipError_t dgx_attn_batch_ex(const void *Q, int q_dtype, const void *Kc, const v
                              long kv_stride, const unsigned *anc, int max_pos, int chunk, hipStream_t st, float scale,
                              int window, int kv_cap);
 /* Prefill with explicit key split (kv_split = 0: none; else a multiple of 64, partials + combine for rows that
- * span splits) over nseq sequences of Sq tokens at (base_b ? base_b[s] : base) + i. Uses the flash scratch
- * (grown in the call when needed). Native form of launch_flash_attn_v2 (attention_flash_v2.cuh:284-292). */
+ * span splits; -1: chosen by the library, a split only when the unsplit grid fills at most half the CUs, e.g. a
+ * short chunk over a long prefix; the choice depends on the launch's own shape, so a row's bits then depend on how
+ * the prompt is chunked) over nseq sequences of Sq tokens at (base_b ? base_b[s] : base) + i. Uses the flash
+ * scratch (grown in the call when needed). Native form of launch_flash_attn_v2 (attention_flash_v2.cuh:284-292). */
 hipError_t dgx_attn_prefill(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
                             int o_dtype, float *lse, int nseq, int Sq, int NQ, int NKV, int HD, const int *base_b,
                             int base, long kv_stride, int max_pos, int kv_split, hipStream_t st, float scale,

@@ -57,14 +57,28 @@ def test_config3_causal_prefill(kv_split):
     _check(O, qv, k, v, toks, Sq, 0, NQ, NKV, HD, f"config3 split={kv_split}", lse=lse)
 
 
-def test_config3_chunked_prefill():
-    """BASELINE config 3 chunked variant: 512 queries over a 4096-token cached prefix plus themselves."""
+@pytest.mark.parametrize("kv_split", [1024, -1])
+def test_config3_chunked_prefill(kv_split):
+    """BASELINE config 3 chunked variant: 512 queries over a 4096-token cached prefix plus themselves, with an
+    explicit key split and with the library's choice (-1)."""
     Sq, base, NQ, NKV, HD = 512, 4096, 16, 8, 256
     q, qv, k, kd, v, vd = _inputs(6, Sq, base, NQ, NKV, HD, 2)
     Q = dev(qv, torch.bfloat16); O = torch.empty(Sq * NQ * HD, device="cuda", dtype=torch.bfloat16)
-    A.attn_prefill(Q, kd, vd, O, 1, Sq, NQ, NKV, HD, base=base, kv_split=1024)
+    A.attn_prefill(Q, kd, vd, O, 1, Sq, NQ, NKV, HD, base=base, kv_split=kv_split)
     torch.cuda.synchronize()
-    _check(O, qv, k, v, _sample_tokens(Sq, base, 0), Sq, base, NQ, NKV, HD, "config3 chunked")
+    _check(O, qv, k, v, _sample_tokens(Sq, base, 0), Sq, base, NQ, NKV, HD, f"config3 chunked split {kv_split}")
+
+
+def test_auto_split_leaves_full_grids_unsplit():
+    """kv_split = -1 keeps a grid that fills the CUs unsplit: config 3 (256 equal workgroups) is bit-identical."""
+    Sq, NQ, NKV, HD = 1024, 16, 8, 256
+    q, qv, k, kd, v, vd = _inputs(3, Sq, 0, NQ, NKV, HD, 2)
+    Q = dev(qv, torch.bfloat16)
+    O0 = torch.empty(Sq * NQ * HD, device="cuda", dtype=torch.bfloat16); O1 = torch.empty_like(O0)
+    A.attn_prefill(Q, kd, vd, O0, 1, Sq, NQ, NKV, HD, kv_split=0)
+    A.attn_prefill(Q, kd, vd, O1, 1, Sq, NQ, NKV, HD, kv_split=-1)
+    torch.cuda.synchronize()
+    assert torch.equal(O0.view(torch.int16), O1.view(torch.int16))
 
 
 def test_config4_sliding_prefill():
