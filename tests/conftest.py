@@ -2,7 +2,7 @@ import os
 import sys
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-for sub in ("", "dgx-serving_amd", "oracle", "tests"):
+for sub in ("", "dgx-serving_amd", "oracle", "tests", os.path.join("tests", "golden")):
     p = os.path.join(ROOT, sub)
     if p not in sys.path:
         sys.path.insert(0, p)
