@@ -698,7 +698,7 @@ __global__ void __launch_bounds__(256) verify_kernel(const SplitArgs a) {
 }
 
 // LSE combine: one wave per (row, head).
-constexpr int kCombineWaves = 4;
+constexpr int kCombineWaves = 2;       // two waves per workgroup: the (row, head) waves spread over more CUs
 template <int HD>
 __global__ void __launch_bounds__(kCombineWaves * 64) combine_kernel(const Problem p, const Partials part, int C) {
     const int rh = blockIdx.x * kCombineWaves + (threadIdx.x >> 6);
