@@ -1,10 +1,10 @@
 """Benchmark of the MI355X attention hot path (BASELINE.json metric).
 
-Headline (`value`): batched split-KV decode at BASELINE config 2 - B=16, Hq=24, Hkv=4, hd=256, f16 KV cache
+Headline (`value`): batched split-KV decode at BASELINE.json config 2 - B=16, Hq=24, Hkv=4, hd=256, f16 KV cache
 [16, 8192, 4, 256], ragged context lengths L_b ~ U[256, 8192] (seeded), split 512 + LSE combine, one query token
 per sequence - as algorithmic HBM GB/s: bytes = sum_b L_b * Hkv * hd * 2 (K and V) * 2 B + |Q| + |O|.
 Alongside: causal flash prefill at config 3 (T=1024, Hq=16, Hkv=8, hd=256, bf16) as TFLOP/s with
-flops = 4 * hd * Hq * sum of attended keys, and the other BASELINE configs in µs per layer call.
+flops = 4 * hd * Hq * sum of attended keys, and the other BASELINE.json configs in µs per layer call.
 A step is one layer call (the split kernel plus the LSE combine kernel for decode).
 
 Timing: W untimed warm-up steps, then exactly K steps between torch.cuda.synchronize() calls, measured with

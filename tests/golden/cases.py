@@ -19,7 +19,7 @@ def _hash(*arrays):
 
 
 def case_config1():
-    """BASELINE config 1: B=1, Hq=16, Hkv=4, hd=128, L=512, f16 Q/K/V ~ N(0,1), scale 1/sqrt(128)."""
+    """BASELINE.json config 1: B=1, Hq=16, Hkv=4, hd=128, L=512, f16 Q/K/V ~ N(0,1), scale 1/sqrt(128)."""
     NQ, NKV, HD, L, dt = 16, 4, 128, 512, 1
     q, qb = oracle.round_to(oracle.gen_normal(101, NQ * HD), dt)
     k, kb = oracle.round_to(oracle.gen_normal(202, L * NKV * HD), dt)

@@ -21,7 +21,7 @@ def _bits(t):
 
 @pytest.mark.parametrize("kvdt", [1, 2])
 def test_config1_decode(kvdt):
-    """BASELINE config 1: B=1, Hq=16, Hkv=4, hd=128, L=512, N(0,1) inputs, scale 1/sqrt(128)."""
+    """BASELINE.json config 1: B=1, Hq=16, Hkv=4, hd=128, L=512, N(0,1) inputs, scale 1/sqrt(128)."""
     NQ, NKV, HD, L = 16, 4, 128, 512
     qv, _ = oracle.round_to(oracle.gen_normal(101, NQ * HD), kvdt)
     kv, kd = normal_cache(202, 1, L, NKV, HD, [L], 1.0, kvdt)
@@ -51,7 +51,7 @@ def _config2(seed=7, B=16, NQ=24, NKV=4, HD=256, max_len=8192, lo=256, kvdt=1):
 
 @pytest.mark.parametrize("chunk", [512, 256])
 def test_config2_batched_ragged(chunk):
-    """BASELINE config 2 at full size: B=16, Hq=24, Hkv=4, hd=256, f16 KV [16,8192,4,256], L~U[256,8192]."""
+    """BASELINE.json config 2 at full size: B=16, Hq=24, Hkv=4, hd=256, f16 KV [16,8192,4,256], L~U[256,8192]."""
     B, NQ, NKV, HD, ML = 16, 24, 4, 256, 8192
     lens, q, kv, kd, vv, vd = _config2()
     pos = (lens - 1).astype(np.int32)

@@ -46,7 +46,7 @@ def _check(O, q, k, v, toks, Sq, base, NQ, NKV, HD, what, scale=0.0, window=0, l
 
 @pytest.mark.parametrize("kv_split", [0, 256, 512])
 def test_config3_causal_prefill(kv_split):
-    """BASELINE config 3: B=1, T=1024, Hq=16, Hkv=8, hd=256, bf16 Q/K/V ~ N(0,1), causal, bf16 output."""
+    """BASELINE.json config 3: B=1, T=1024, Hq=16, Hkv=8, hd=256, bf16 Q/K/V ~ N(0,1), causal, bf16 output."""
     Sq, NQ, NKV, HD = 1024, 16, 8, 256
     q, qv, k, kd, v, vd = _inputs(5, Sq, 0, NQ, NKV, HD, 2)
     Q = dev(qv, torch.bfloat16); O = torch.empty(Sq * NQ * HD, device="cuda", dtype=torch.bfloat16)
@@ -59,7 +59,7 @@ def test_config3_causal_prefill(kv_split):
 
 @pytest.mark.parametrize("kv_split", [1024, -1])
 def test_config3_chunked_prefill(kv_split):
-    """BASELINE config 3 chunked variant: 512 queries over a 4096-token cached prefix plus themselves, with an
+    """BASELINE.json config 3 chunked variant: 512 queries over a 4096-token cached prefix plus themselves, with an
     explicit key split and with the library's choice (-1)."""
     Sq, base, NQ, NKV, HD = 512, 4096, 16, 8, 256
     q, qv, k, kd, v, vd = _inputs(6, Sq, base, NQ, NKV, HD, 2)
@@ -82,7 +82,7 @@ def test_auto_split_leaves_full_grids_unsplit():
 
 
 def test_config4_sliding_prefill():
-    """BASELINE config 4a: sliding window 1024, T=4096, Hq=16, Hkv=8, hd=256, bf16."""
+    """BASELINE.json config 4a: sliding window 1024, T=4096, Hq=16, Hkv=8, hd=256, bf16."""
     Sq, NQ, NKV, HD, W = 4096, 16, 8, 256, 1024
     q, qv, k, kd, v, vd = _inputs(8, Sq, 0, NQ, NKV, HD, 2)
     Q = dev(qv, torch.bfloat16); O = torch.empty(Sq * NQ * HD, device="cuda", dtype=torch.bfloat16)

@@ -52,7 +52,7 @@ def test_chain_equals_causal_and_branch_equals_linear():
 
 @pytest.mark.parametrize("tree", ["random8", "kw9"])
 def test_config5_batched_tree_verify(tree):
-    """BASELINE config 5: B=16, tree nodes per sequence (seeded 2-wide depth<=7 tree of 8 nodes, or the
+    """BASELINE.json config 5: B=16, tree nodes per sequence (seeded 2-wide depth<=7 tree of 8 nodes, or the
     reference's K7W2 shape of 9 nodes), committed L ~ U[2048, 16384], Hq=24, Hkv=4, hd=256, f16 KV."""
     B, NQ, NKV, HD = 16, 24, 4, 256
     committed = oracle.gen_uniform_int(55, 2048, 16384, B)
