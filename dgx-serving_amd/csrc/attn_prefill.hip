@@ -92,9 +92,10 @@ struct PrefCfg {
 };
 
 // Slot swizzle of key row k: 16-byte column c of key k sits in slot c ^ swz(k), a permutation of the low 4 key
-// bits. It spreads the 16 keys of a K fragment read over 16 different bank groups and the 4 keys x 2 columns of a
-// V transpose read (keys 4g..4g+3) over 8.
-__device__ __forceinline__ int swz(int k) { return ((k & 3) << 1) | ((k >> 2) & 1) | (k & 8); }
+// bits (keys 0-7 to the even slots, 8-15 to the odd ones). It spreads the 16 keys of a K fragment read over the
+// 16 slots of a 256-byte bank row, and the 8 keys x 2 columns that the 32 lanes of a half V transpose read
+// (keys 4g..4g+3 for g = 0, 1 or g = 2, 3) over all 16 slots as well.
+__device__ __forceinline__ int swz(int k) { return ((k & 7) << 1) | ((k >> 3) & 1); }
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void glb_void;

@@ -515,7 +515,7 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
 // ring with gfx950 direct-to-LDS loads (no staging registers, so more tiles in flight per workgroup at the same
 // occupancy), rows unpadded with their 16-byte slots XOR-swizzled by the key (swz below). Wave w owns row block w
 // (all head dims); the wave past the last row block only loads.
-__device__ __forceinline__ int vswz(int k) { return ((k & 3) << 1) | ((k >> 2) & 1) | (k & 8); }
+__device__ __forceinline__ int vswz(int k) { return ((k & 7) << 1) | ((k >> 3) & 1); }
 typedef __attribute__((address_space(3))) void vlds_void;
 typedef __attribute__((address_space(1))) void vglb_void;
 
