@@ -93,3 +93,32 @@ def test_random_prefill(seed):
                                window=c["window"])
     assert_close(O.float().cpu().numpy().reshape(Sq, NQ, HD), ref, f"case {seed} {c}",
                  lse.cpu().numpy().reshape(Sq, NQ), ref_lse)
+
+
+@pytest.mark.parametrize("T,tree", [(1, False), (8, True), (3, False)])
+def test_many_sequences(T, tree):
+    """More than 64 sequences, so the device-side work enumeration (decode items, verify runs) and the combine's
+    run scan cover several 64-lane blocks; short ragged lengths keep the oracle fast."""
+    B, NQ, NKV, HD, kvdt = 100, 16, 2, 128, 1
+    committed = np.random.default_rng(77 + T).integers(0, 700, size=B).astype(np.int32)
+    ML = int(committed.max()) + T
+    lens = committed + T
+    kv, kd = normal_cache(91, B, ML, NKV, HD, lens, 0.5, kvdt)
+    vv, vd = normal_cache(92, B, ML, NKV, HD, lens, 0.5, kvdt)
+    q = oracle.gen_normal(93, B * T * NQ * HD)
+    qr, _ = oracle.round_to(q, kvdt)
+    anc = None
+    if tree:
+        anc = np.stack([oracle.tree_anc(oracle.tree_random(500 + b, T, 2, 7)[0]) for b in range(B)]).astype(np.uint32)
+    max_pos = int((committed + T - 1).max())
+    A.split_reserve(B * T * 2, NQ, max_pos + 1, HD)
+    O = torch.empty(B * T * NQ * HD, device="cuda"); lse = torch.empty(B * T * NQ, device="cuda")
+    A.attn_batch(dev(q), kd, vd, O, B, T, NQ, NKV, HD, dev(committed), ML * NKV * HD, max_pos, chunk=256,
+                 anc=None if anc is None else dev(anc.reshape(-1).view(np.int32)), lse=lse)
+    torch.cuda.synchronize()
+    pos = (committed[:, None] + np.arange(T)[None, :]).reshape(-1)
+    off = np.repeat(np.arange(B, dtype=np.int64) * ML * NKV * HD, T)
+    ref, ref_lse = oracle_rows(qr, kv, vv, off, pos, NQ, NKV, HD, anc=None if anc is None else anc.reshape(-1),
+                               tree_base=None if anc is None else np.repeat(committed, T))
+    assert_close(O.cpu().numpy().reshape(B * T, NQ, HD), ref, f"B={B} T={T}", lse.cpu().numpy().reshape(-1, NQ),
+                 ref_lse)
