@@ -56,36 +56,44 @@ extern "C" hipError_t dgx_dtrace_read(void *host, size_t bytes) {
 
 // Work item blockIdx.x -> (sequence, chunk c, kv head blockIdx.x % NKV), enumerating only the chunks that hold keys
 // of the sequence's tokens (kv head fastest): the workgroups with work come first in launch order and the dispatcher
-// spreads them over all CUs; the tail of the upper-bound grid (false) exits at once.
+// spreads them over all CUs; the tail of the upper-bound grid (false) exits at once. Two phases: first every chunk
+// of each sequence but its last, then the last chunks (the partial ones). The dispatcher hands workgroups out in
+// index order and a CU that receives more workgroups than the others shares its bandwidth among them, so the short
+// items go last, where they land on the CUs that get a third workgroup (measured: a CU with three full items runs
+// 20% longer than one with two).
 __device__ __forceinline__ bool find_item(const Problem &p, int C, int &seq, int &c) {
     const int lane_ = threadIdx.x & 63, cmax = p.max_pos / C;
     int rest = (int)blockIdx.x / p.NKV;
     seq = -1; c = 0;
-    for (int s0 = 0; s0 < p.nseq; s0 += 64) {
-        int n = 0, first = 0;
-        if (s0 + lane_ < p.nseq) {
-            int lo_s = INT_MAX, hi_s = 0;                  // key range of the sequence's tokens
-            for (int t = 0; t < p.T; t++) {
-                const int ps = tok_pos(p, s0 + lane_, t);
-                lo_s = min(lo_s, win_lo(ps, p.window)); hi_s = max(hi_s, ps + 1);
+    for (int phase = 0; phase < 2; phase++) {
+        for (int s0 = 0; s0 < p.nseq; s0 += 64) {
+            int n = 0, first = 0;
+            if (s0 + lane_ < p.nseq) {
+                int lo_s = INT_MAX, hi_s = 0;              // key range of the sequence's tokens
+                for (int t = 0; t < p.T; t++) {
+                    const int ps = tok_pos(p, s0 + lane_, t);
+                    lo_s = min(lo_s, win_lo(ps, p.window)); hi_s = max(hi_s, ps + 1);
+                }
+                first = lo_s / C;
+                n = max(0, min((hi_s - 1) / C, cmax) - first + 1);
             }
-            first = lo_s / C;
-            n = max(0, min((hi_s - 1) / C, cmax) - first + 1);
-        }
-        int incl = n;                                      // inclusive prefix sum over the 64 lanes
+            const int m = phase == 0 ? max(n - 1, 0) : min(n, 1);   // items of this sequence in this phase
+            int incl = m;                                  // inclusive prefix sum over the 64 lanes
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o);
-            if (lane_ >= o) incl += y;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(incl, o);
+                if (lane_ >= o) incl += y;
+            }
+            const unsigned long long hit = __ballot(incl > rest);
+            if (hit) {
+                const int l = __builtin_ctzll(hit);
+                seq = s0 + l;
+                c = phase == 0 ? __shfl(first, l) + rest - (__shfl(incl, l) - __shfl(m, l))
+                               : __shfl(first, l) + __shfl(n, l) - 1;
+                return true;
+            }
+            rest -= __shfl(incl, 63);
         }
-        const unsigned long long hit = __ballot(incl > rest);
-        if (hit) {
-            const int l = __builtin_ctzll(hit);
-            seq = s0 + l;
-            c = __shfl(first, l) + rest - (__shfl(incl, l) - __shfl(n, l));
-            return true;
-        }
-        rest -= __shfl(incl, 63);
     }
     return false;
 }
