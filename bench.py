@@ -266,6 +266,12 @@ def main():
         extra["prefill_chunked_512_over_4096"] = dict(us=round(cms * 1e3, 2), tflops=round(cfl / (cms * 1e-3) / 1e12, 2))
         sms, sfl = run_prefill(max(args.steps // 4, 10), args.warmup, T=4096, window=1024, kv_split=0)
         extra["prefill_sliding_T4096_w1024"] = dict(us=round(sms * 1e3, 2), tflops=round(sfl / (sms * 1e-3) / 1e12, 2))
+        # The same decode workload at a split of 384 keys: its ~776 chunk items fill the 256 CUs three deep, where
+        # the 564 items of the 512 split leave 52 CUs a third item (the headline keeps the configured 512 split).
+        ams, aby, akms = run_decode(w, args.steps, args.warmup, chunk=384, copies=3)
+        extra["decode_split384"] = dict(us=round(ams * 1e3, 2), gbs=round(aby / (ams * 1e-3) / 1e9, 1),
+                                        kernel_us=round(akms * 1e3, 2),
+                                        kernel_frac_hbm=round(aby / (akms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
         dms, dby = run_sliding_decode(args.steps, args.warmup)
         extra["decode_sliding_B8_w1024"] = dict(us=round(dms * 1e3, 2), gbs=round(dby / (dms * 1e-3) / 1e9, 1))
         fms, fby = run_decode_fp32(max(args.steps // 10, 5), 2, w)

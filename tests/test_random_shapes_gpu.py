@@ -122,3 +122,27 @@ def test_many_sequences(T, tree):
                                tree_base=None if anc is None else np.repeat(committed, T))
     assert_close(O.cpu().numpy().reshape(B * T, NQ, HD), ref, f"B={B} T={T}", lse.cpu().numpy().reshape(-1, NQ),
                  ref_lse)
+
+
+@pytest.mark.parametrize("chunk,T", [(384, 1), (224, 1), (384, 3)])
+def test_chunks_off_powers_of_two(chunk, T):
+    """Chunk sizes that are multiples of 32 but not powers of two (the streaming kernel's two key lanes then split
+    a chunk into unequal tile counts, and chunk boundaries fall inside 64-key blocks)."""
+    B, NQ, NKV, HD, kvdt = 6, 24, 4, 256, 1
+    committed = np.array([0, 383, 384, 1000, 2047, 3001], np.int32)
+    ML = int(committed.max()) + T
+    lens = committed + T
+    kv, kd = normal_cache(31, B, ML, NKV, HD, lens, 0.5, kvdt)
+    vv, vd = normal_cache(32, B, ML, NKV, HD, lens, 0.5, kvdt)
+    q = oracle.gen_normal(33, B * T * NQ * HD)
+    qr, _ = oracle.round_to(q, kvdt)
+    max_pos = int((committed + T - 1).max())
+    A.split_reserve(B * T * -(-A.split_chunk() // chunk), NQ, max_pos + 1, HD)
+    O = torch.empty(B * T * NQ * HD, device="cuda"); lse = torch.empty(B * T * NQ, device="cuda")
+    A.attn_batch(dev(q), kd, vd, O, B, T, NQ, NKV, HD, dev(committed), ML * NKV * HD, max_pos, chunk=chunk, lse=lse)
+    torch.cuda.synchronize()
+    pos = (committed[:, None] + np.arange(T)[None, :]).reshape(-1)
+    off = np.repeat(np.arange(B, dtype=np.int64) * ML * NKV * HD, T)
+    ref, ref_lse = oracle_rows(qr, kv, vv, off, pos, NQ, NKV, HD)
+    assert_close(O.cpu().numpy().reshape(B * T, NQ, HD), ref, f"chunk={chunk} T={T}", lse.cpu().numpy().reshape(-1, NQ),
+                 ref_lse)
