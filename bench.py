@@ -162,6 +162,7 @@ def run_decode_fp32(steps, warmup, w):
     B, NQ, NKV, HD, ML = w["B"], w["NQ"], w["NKV"], w["HD"], w["ML"]
     K = w["K"].float(); V = w["V"].float()
     Q = w["Q"].float(); O = torch.empty_like(Q)
+    A.flash_reserve_partials(B * NQ * (ML // 512 + 1), HD)     # the fp32 MFMA kernel's partials, before timing
     ms = timed(lambda: A.attn_decode_batch(Q, K, V, O, B, NQ, NKV, HD, 0, ML * NKV * HD, base_b=w["pos"]), steps,
                warmup)
     del K, V
@@ -189,8 +190,20 @@ def run_kv_append(steps, warmup, B=16, T=1, NKV=4, HD=256, ML=8192, kvdt=1):
     return fused, looped, B * T * row * (4 + 2) * 2
 
 
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(w):
-    """Oracle fp32 host attention over the full decode workload, all host threads, on the GPU's inputs."""
+    """Oracle fp32 host attention (restating tests/test_kernels.cu:94-108) over the full decode workload, on the
+    GPU's inputs, at 1 thread, 8 threads (the reference harness's cap, tests/test_flash_gemma.cu:342) and 16 threads
+    (this box's CPU share per GPU; the machine may list more CPUs). `value` is the 16-thread rate."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     B, NQ, NKV, HD, ML = w["B"], w["NQ"], w["NKV"], w["HD"], w["ML"]
@@ -200,14 +213,43 @@ def cpu_baseline(w):
     V = w["V"][:, :Lmax].float().cpu().numpy()
     q = w["Q"].float().cpu().numpy()
     kv_off = np.arange(B, dtype=np.int64) * Lmax * NKV * HD
-    threads = min(os.cpu_count() or 1, 16)
-    t0 = time.perf_counter()
-    oracle.attention(q, K, V, kv_off, lens - 1, NQ, NKV, HD, mode=1, nthreads=threads)
-    dt = time.perf_counter() - t0
     nbytes = int(lens.sum()) * NKV * HD * 4 + 2 * B * NQ * HD * 2
-    return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    rates = {}
+    for threads in (1, 8, 16):
+        t0 = time.perf_counter()
+        oracle.attention(q, K, V, kv_off, lens - 1, NQ, NKV, HD, mode=1, nthreads=threads)
+        dt = time.perf_counter() - t0
+        rates[threads] = (nbytes / dt / 1e9, dt)
+    v16, dt16 = rates[16]
+    return dict(value=round(v16, 3), unit="GB/s", cores=16, kind="port",
+                threads_1_gbs=round(rates[1][0], 3), threads_8_gbs=round(rates[8][0], 3),
+                threads_16_gbs=round(v16, 3), host_cpus=os.cpu_count(), affinity_cpus=affinity,
+                cpu_model=_cpu_model(),
                 sample=f"full decode workload (16 rows x 24 heads, sum L = {int(lens.sum())} keys), fp32 host "
-                       f"attention (fp64 dot, fp32 softmax) over {threads} threads, {dt * 1e3:.1f} ms per call")
+                       f"attention (fp64 dot, fp32 softmax); ms per call at 1/8/16 threads: "
+                       f"{rates[1][1] * 1e3:.1f}/{rates[8][1] * 1e3:.1f}/{dt16 * 1e3:.1f}")
+
+
+def run_global_decode(steps, warmup, seed=13):
+    """Gemma4-12B global layer decode (tools/autotune/profiles/gemma4-12b.json: 16 q-heads, 1 KV head, head_dim
+    512): B=8, ragged L~U[1024, 32768], bf16 KV and Q/O, no window, split 512. Returns (ms, bytes, kernel ms)."""
+    B, NQ, NKV, HD, ML = 8, 16, 1, 512, 32768
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(1024, ML, size=B, endpoint=True).astype(np.int32)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    K = torch.randn(B, ML, NKV, HD, device="cuda", generator=g).bfloat16()
+    V = torch.randn(B, ML, NKV, HD, device="cuda", generator=g).bfloat16()
+    Q = torch.randn(B * NQ * HD, device="cuda", generator=g).bfloat16()
+    O = torch.empty_like(Q)
+    pos = torch.from_numpy(lens - 1).cuda()
+    A.split_reserve(B, NQ, ML, HD)
+    fn = lambda: A.attn_batch(Q, K, V, O, B, 1, NQ, NKV, HD, pos, ML * NKV * HD, int(lens.max()) - 1, chunk=512)
+    ms, kms = timed(fn, steps, warmup, kernel=True)
+    return ms, int(lens.sum()) * NKV * HD * 2 * 2 + 2 * Q.numel() * 2, kms
 
 
 def traffic_from_profile():
@@ -281,6 +323,13 @@ def main():
                                       gbs=round(aby / (ams * 1e-3) / 1e9, 1))
         tms, tby = run_tree(args.steps, args.warmup)
         extra["tree_verify_B16x8"] = dict(us=round(tms * 1e3, 2), gbs=round(tby / (tms * 1e-3) / 1e9, 1))
+        gms, gby, gkms = run_global_decode(args.steps, args.warmup)
+        extra["decode_global_hd512_B8"] = dict(us=round(gms * 1e3, 2), gbs=round(gby / (gms * 1e-3) / 1e9, 1),
+                                               kernel_us=round(gkms * 1e3, 2),
+                                               kernel_frac_hbm=round(gby / (gkms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+        pms2, pfl2 = run_prefill(args.steps, args.warmup, T=1024, NQ=16, NKV=1, HD=512)
+        extra["prefill_global_hd512_T1024"] = dict(us=round(pms2 * 1e3, 2), tflops=round(pfl2 / (pms2 * 1e-3) / 1e12, 2),
+                                                   frac_bf16_peak=round(pfl2 / (pms2 * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
     out = {
         "metric": "decode-attn HBM GB/s (B16 ragged <=8K) + prefill-attn TFLOP/s (T=1024)",
         "value": round(gbs, 1),

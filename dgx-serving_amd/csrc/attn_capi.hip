@@ -64,8 +64,8 @@ int parse_chunk() {
     int c = 256;                                  // MI355X default (the GB10 reference defaults to 64)
     if (const char *v = knob_raw("G4_ATTN_CHUNK")) {
         c = atoi(v);
-        if (c != 32 && c != 64 && c != 128 && c != 256 && c != 512) {
-            fprintf(stderr, "Invalid G4_ATTN_CHUNK=%s (32, 64, 128, 256 or 512)\n", v);
+        if (c != 32 && c != 64 && c != 128 && c != 256) {             // the reference's value set
+            fprintf(stderr, "Invalid G4_ATTN_CHUNK=%s (32, 64, 128 or 256)\n", v);
             return -1;
         }
     }
@@ -175,23 +175,28 @@ hipError_t run_split(const Problem &p, int chunk, Pool &pool, int ns_cap, hipStr
 }
 
 // fp32 caches, up to 16 rows per KV head, no reverse-order diagnostic: the fp32 MFMA streaming kernel + combine on
-// the given pool (grown here when `grow`, as the reference's flash path grows its scratch inside the call).
+// the given pool. Never allocates: the caller checks f32_reserved first (the reference's fp32 launchers use only
+// shared memory, attention.cuh:137-198, so these calls must stay capture-safe and allocation-free).
 constexpr int kF32Chunk = 512;
 bool f32_fast(const Problem &p) { return decode_f32_supported(p) && !knob_on("G4_ATTN_DIAG_REVERSE"); }
-hipError_t run_f32(const Problem &p, Pool &pool, bool grow, hipStream_t st) {
-    const int ns = p.max_pos / kF32Chunk + 1;
-    const size_t need = (size_t)p.nseq * p.T * p.NQ * ns;
-    if (grow) {
-        std::lock_guard<std::mutex> lock(g_pool_mu);
-        hipError_t e = pool_grow(pool, need, (size_t)p.HD);
-        if (e != hipSuccess) return e;
-    } else if (need > pool.cap || need * p.HD > pool.acc_cap) {
-        return hipErrorInvalidValue;
-    }
-    Partials part{pool.m, pool.l, pool.acc, ns};
+size_t f32_need(const Problem &p) { return (size_t)p.nseq * p.T * p.NQ * (size_t)(p.max_pos / kF32Chunk + 1); }
+bool f32_reserved(const Problem &p, const Pool &pool) {
+    const size_t need = f32_need(p);
+    return need <= pool.cap && need * (size_t)p.HD <= pool.acc_cap;
+}
+hipError_t run_f32(const Problem &p, const Pool &pool, hipStream_t st) {
+    Partials part{pool.m, pool.l, pool.acc, p.max_pos / kF32Chunk + 1};
     hipError_t e = timed_launch(st, [&] { return launch_decode_f32(p, kF32Chunk, part, st); });
     if (e != hipSuccess) return e;
     return launch_combine(p, kF32Chunk, part, st);
+}
+// The fp32 drop-in launchers take the MFMA kernel when the flash pool already holds its partials (reserved with
+// dgx_flash_attn_reserve_partials or grown by an earlier flash call), else the scalar kernels.
+bool f32_take_fast(const Problem &p, const Pool *&pool) {
+    if (!f32_fast(p)) return false;
+    Pool *pl; if (pool_for(g_flash, pl) != hipSuccess) return false;
+    pool = pl;
+    return f32_reserved(p, *pl);
 }
 
 }  // namespace
@@ -248,7 +253,7 @@ hipError_t dgx_attn_decode_split(const float *Q, const void *Kc, const void *Vc,
         const Problem pf = make_problem(Q, DT_FP32, Kc, Vc, DT_FP32, O, DT_FP32, lse, rows, 1, NQ, NKV, HD, kv_stride, 0,
                                         base, pos_step, pos_arr, nullptr, max_pos, scale, window);
         // (the reservation, made for the library chunk <= 512, always covers the streaming kernel's 512-key chunks)
-        if (f32_fast(pf)) return run_f32(pf, *pool, false, st);
+        if (f32_fast(pf) && f32_reserved(pf, *pool)) return run_f32(pf, *pool, st);
         if (lse) return hipErrorInvalidValue;   // the fp32 path keeps the reference's outputs (O only)
         return launch_scalar_rows(Q, (const float *)Kc, (const float *)Vc, O, rows, NQ, NKV, HD, base, pos_step, pos_arr,
                                   kv_stride, resolve_scale(scale, HD), window, knob_on("G4_ATTN_DIAG_REVERSE") ? 1 : 0, st);
@@ -292,11 +297,18 @@ hipError_t dgx_flash_attn(const float *Q, const void *Kc, const void *Vc, int kv
     Problem p = make_problem(Q, DT_FP32, Kc, Vc, kv_dtype, O, DT_FP32, lse, 1, Sq, NQ, NKV, HD, 0, 1, base, 1, nullptr,
                              anc, base + Sq - 1, 1.f, window);
     p.scale = sc;
-    if (Sq <= kFlashShortSq) {
+    if (Sq <= kFlashShortSq || anc) {
+        // Short runs and every tree-masked run take the split kernel. A tree run longer than 32 tokens keeps the
+        // reference's rule: nodes at bit 32 and beyond are never attended (attention_flash.cuh:177), and its
+        // partials grow the pool here as the reference's flash launch does.
         const int ns = (base + Sq - 1) / kFlashChunk + 1;
+        if (Sq > kFlashShortSq) {
+            std::lock_guard<std::mutex> lock(g_pool_mu);
+            e = pool_grow(*pool, (size_t)Sq * NQ * ns, (size_t)HD);
+            if (e != hipSuccess) return e;
+        }
         return run_split(p, kFlashChunk, *pool, ns, st);
     }
-    if (anc) return hipErrorInvalidValue;      // a tree mask covers at most 32 nodes (attention_flash.cuh:177)
     // No key split: the prefill kernel balances causal work by pairing query tiles, and a row's result does not
     // depend on how the prompt is chunked.
     return timed_launch(st, [&] { return launch_prefill(p, 0, Partials{nullptr, nullptr, nullptr, 0}, st); });
@@ -322,10 +334,8 @@ hipError_t dgx_attn(const float *Q, const float *K, const float *V, float *O, in
     if (valid_hd(HD)) {                                   // short prompts: query i attends keys 0..i
         const Problem p = make_problem(Q, DT_FP32, K, V, DT_FP32, O, DT_FP32, nullptr, 1, S, NQ, NKV, HD, 0, 1, 0, 1,
                                        nullptr, nullptr, S - 1, scale, window);
-        if (f32_fast(p)) {
-            Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
-            return run_f32(p, *pool, true, st);
-        }
+        const Pool *pool = nullptr;
+        if (f32_take_fast(p, pool)) return run_f32(p, *pool, st);
     }
     return launch_scalar_prefill(Q, K, V, O, S, NQ, NKV, HD, resolve_scale(scale, HD), window < 0 ? 0 : window, st);
 }
@@ -338,10 +348,8 @@ hipError_t dgx_attn_decode(const float *Q, const float *Kc, const float *Vc, flo
     if (valid_hd(HD)) {
         const Problem p = make_problem(Q, DT_FP32, Kc, Vc, DT_FP32, O, DT_FP32, nullptr, 1, Sq, NQ, NKV, HD, 0, 1,
                                        base, 1, nullptr, nullptr, base + Sq - 1, scale, window);
-        if (f32_fast(p)) {
-            Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
-            return run_f32(p, *pool, true, st);
-        }
+        const Pool *pool = nullptr;
+        if (f32_take_fast(p, pool)) return run_f32(p, *pool, st);
     }
     return launch_scalar_decode(Q, Kc, Vc, O, 1, Sq, NQ, NKV, HD, base, 0, nullptr, resolve_scale(scale, HD),
                                 window < 0 ? 0 : window, knob_on("G4_ATTN_DIAG_REVERSE") ? 1 : 0, st);
@@ -361,10 +369,8 @@ hipError_t dgx_attn_decode_batch(const float *Q, const float *Kc, const float *V
         const int max_pos = base_b ? (int)cap_rows - 1 : base;
         const Problem p = make_problem(Q, DT_FP32, Kc, Vc, DT_FP32, O, DT_FP32, nullptr, B, 1, NQ, NKV, HD, kv_stride, 1,
                                        base, 1, base_b, nullptr, max_pos, scale, window);
-        if (f32_fast(p)) {
-            Pool *pool; hipError_t e = pool_for(g_flash, pool); if (e != hipSuccess) return e;
-            return run_f32(p, *pool, true, st);
-        }
+        const Pool *pool = nullptr;
+        if (f32_take_fast(p, pool)) return run_f32(p, *pool, st);
     }
     return launch_scalar_decode(Q, Kc, Vc, O, B, 1, NQ, NKV, HD, base, kv_stride, base_b, resolve_scale(scale, HD),
                                 window < 0 ? 0 : window, knob_on("G4_ATTN_DIAG_REVERSE") ? 1 : 0, st);

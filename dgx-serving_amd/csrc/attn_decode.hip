@@ -47,12 +47,6 @@ struct DecodeCfg {
     static constexpr size_t LDS = LDS_Q + (LDS_V > LDS_MERGE ? LDS_V : LDS_MERGE);
 };
 
-#ifdef DGX_TRACE
-__device__ unsigned long long g_dtrace[1 << 16][4];
-extern "C" hipError_t dgx_dtrace_read(void *host, size_t bytes) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dtrace), bytes, 0, hipMemcpyDeviceToHost);
-}
-#endif
 
 // Work item blockIdx.x -> (sequence, chunk c, kv head blockIdx.x % NKV), enumerating only the chunks that hold keys
 // of the sequence's tokens (kv head fastest): the workgroups with work come first in launch order and the dispatcher
@@ -100,9 +94,6 @@ __device__ __forceinline__ bool find_item(const Problem &p, int C, int &seq, int
 
 template <int HD, int NKL_, int RW_, int KVT, int QT, bool EARLY>
 __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const DecodeArgs a) {
-#ifdef DGX_TRACE
-    const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
-#endif
     using Cf = DecodeCfg<HD, NKL_, RW_>;
     constexpr int NW = Cf::NW, NKL = Cf::NKL, RW = Cf::RW, KT = Cf::KT;
     constexpr bool F16 = OpIsF16<KVT>::value;
@@ -271,18 +262,6 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
         compute(k, kb, vb);
     }
     l = sum_over_groups(l);
-#ifdef DGX_TRACE
-    if (lane == 0) {
-        const size_t bid = (((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 4 + wave;
-        unsigned xcc, hwid;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
-        g_dtrace[bid & 0xffff][0] = t_start;
-        g_dtrace[bid & 0xffff][1] = __builtin_amdgcn_s_memrealtime();
-        g_dtrace[bid & 0xffff][2] = (j_hi - j_lo + 15) / 16;
-        g_dtrace[bid & 0xffff][3] = (unsigned long long)(xcc & 0xf) | ((unsigned long long)hwid << 4);
-    }
-#endif
 
     // Merge the NKL key-lane states of each row block in key-lane order (LDS, over the tile slices), then write the
     // chunk partial of each row.

@@ -38,17 +38,6 @@
 
 namespace dgx {
 
-#ifdef DGX_TRACE
-// Debug builds only: shader-clock stamps of workgroup 0 ([wave][event]).
-__device__ unsigned long long g_pref_trace[8][256];
-extern "C" hipError_t dgx_pref_trace_read(void *host, size_t bytes) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_pref_trace), bytes, 0, hipMemcpyDeviceToHost);
-}
-#define PTR(ev) do { if (blockIdx.x == 0 && lane == 0 && tr_n < 256) g_pref_trace[wave][tr_n++] = ((unsigned long long)(ev) << 56) | (__builtin_amdgcn_s_memtime() & 0xffffffffffffffull); } while (0)
-#else
-#define PTR(ev) do { } while (0)
-#endif
-
 struct PrefArgs {
     Problem p;
     Partials part;
@@ -139,10 +128,6 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
     const KE *Vb = kv_base<KE>(p, true, seq) + (size_t)kvh * HD;
     // Prefill tokens are consecutive: token t of this sequence sits at position pbase + t.
     const int pbase = __builtin_amdgcn_readfirstlane(p.pos_arr ? p.pos_arr[seq] : p.base);
-#ifdef DGX_TRACE
-    int tr_n = 0;
-#endif
-    PTR(1);
 
     // The two half tiles of this work item (longest first) and their tokens; an empty half has tok1 == tok0.
     const int nhalf_items = a.nitems / a.nsplit;
@@ -227,7 +212,6 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
         wlo = max(win_lo(pf, p.window), j_lo); whi = min(pl, j_hi - 1);
         lo_max = win_lo(pl, p.window); pos_min = pf;
     }
-    PTR(2);
 
     float m[RB], l[RB];
     f32x4 acc[RB][DB];
@@ -251,7 +235,6 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
         wait_steps<DMA ? 2 * NLD : 0>(min(NS - 2, nsteps - 1 - it));
         __syncthreads();                                                // everyone's step it, and step it-1 is consumed
         if (it + NS - 1 < nsteps) issue(it + NS - 1);
-        PTR(3);
         // This wave's keys of the step: NSUB 16-key sub-tiles from jw. QK for all of them first (independent MFMA
         // chains), one softmax update over all of them, then PV.
         const int jw = (s0 + it) * SK + kg * Cf::KT;
@@ -332,12 +315,10 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
 #pragma unroll
                     for (int rb = 0; rb < RB; rb++) acc[rb][d8 + j] = mfma16k16<F16>(v[j], pop[sub][rb], acc[rb][d8 + j]);
             }
-        PTR(4);
     }
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) l[rb] = sum_over_groups(l[rb]);
     __syncthreads();                                                 // every wave is done with the K/V tiles
-    PTR(7);
 
     // Merge the two key-group states of each row (waves kg = 0 and 1 of a row group hold the same rows). Every
     // lane derives the row's M = max m and L = sum l 2^(m - M) from the published (m, l) and scales its
@@ -350,7 +331,6 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
         for (int rb = 0; rb < RB; rb++) { stm[wave * RB * 16 + rb * 16 + ln] = m[rb]; stl[wave * RB * 16 + rb * 16 + ln] = l[rb]; }
     }
     __syncthreads();
-    PTR(9);
     constexpr int DH = DB / 2;                                          // dim blocks per owner
     float *xb = reinterpret_cast<float *>(smem);                        // [rg][owner kg][row][XSTR] (reuses tiles)
     float fsc[RB];
@@ -386,7 +366,6 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
         }
     }
     __syncthreads();
-    PTR(10);
     // Output dims of this wave: blocks [OWN*DH, (OWN+1)*DH) of its accumulator (OWN a constant, so acc stays in
     // registers).
     auto finish = [&](auto own_c) {
@@ -417,7 +396,6 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
     };
     if (kg == 0) finish(std::integral_constant<int, 0>{});
     else finish(std::integral_constant<int, 1>{});
-    PTR(8);
 }
 
 // ---------------------------------------------------------------- host side

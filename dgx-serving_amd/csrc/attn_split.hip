@@ -231,18 +231,9 @@ struct SplitCfg {
     static_assert(CPT >= 1 && (KT * HD / 8) % (NW * 64) == 0, "tile chunks");
 };
 
-#ifdef DGX_TRACE
-__device__ unsigned long long g_trace[1 << 16][4];
-extern "C" hipError_t dgx_trace_read(void *host, size_t bytes) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), bytes, 0, hipMemcpyDeviceToHost);
-}
-#endif
 
 template <int HD, int RB, int KVT, int QT>
 __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
-#ifdef DGX_TRACE
-    const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
-#endif
     using Cf = SplitCfg<HD, RB>;
     constexpr int NW = Cf::NW;
     constexpr bool F16 = OpIsF16<KVT>::value;
@@ -473,19 +464,6 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
             __syncthreads();
         }
     }
-#ifdef DGX_TRACE
-    if (tid == 0) {
-        const size_t bid = ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
-        unsigned xcc, hwid;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hwid));
-        xcc = (xcc & 0xf) | (((hwid >> 8) & 0xf) << 4) | (((hwid >> 12) & 0x7) << 8);   // xcc | cu << 4 | sh,se << 8
-        g_trace[bid & 0xffff][0] = t_start;
-        g_trace[bid & 0xffff][1] = __builtin_amdgcn_s_memrealtime();
-        g_trace[bid & 0xffff][2] = ntile;
-        g_trace[bid & 0xffff][3] = xcc;
-    }
-#endif
 #pragma unroll
     for (int rb = 0; rb < RBW; rb++) l[rb] = sum_over_groups(l[rb]);
     if (!active) return;

@@ -9,7 +9,7 @@ import os
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.environ.get("DGX_ATTN_LIB") or os.path.join(_HERE, "libdgx_attn.so")   # override: alternate builds
+LIB_PATH = os.path.join(_HERE, "libdgx_attn.so")
 
 FP32, F16, BF16 = 0, 1, 2
 _DT = {torch.float32: FP32, torch.float16: F16, torch.bfloat16: BF16}
@@ -108,6 +108,15 @@ def flash_attn(Q, K, V, O, Sq, NQ, NKV, HD, base, anc=None, scale=0.0, window=0,
 def flash_attn_v2(Q, K, V, O, Sq, NQ, NKV, HD, base, scale=0.0, window=0, f16_mma=0, lse=None):
     _ck(lib().dgx_flash_attn_v2(_ptr(Q), _ptr(K), _ptr(V), kv_code(K), _ptr(O), _ptr(lse), Sq, NQ, NKV, HD, base,
                                 _stream(), float(scale), window, f16_mma), "dgx_flash_attn_v2")
+
+
+def flash_reserve(Sq, NQ, base, HD):
+    _ck(lib().dgx_flash_attn_reserve(Sq, NQ, base, HD), "dgx_flash_attn_reserve")
+
+
+def flash_reserve_partials(partials, hd_max):
+    """Pre-size the flash scratch (also what lets the fp32 launchers take the fp32 MFMA kernel)."""
+    _ck(lib().dgx_flash_attn_reserve_partials(partials, hd_max), "dgx_flash_attn_reserve_partials")
 
 
 def attn(Q, K, V, O, S, NQ, NKV, HD, scale=0.0, window=0):

@@ -42,7 +42,8 @@ void dgx_kv_force_fp32(const char *why);
 /* Bytes per stored KV element (4 or 2). Replaces g4_kv_elem(), kernels/kv_store.cuh:42. */
 size_t dgx_kv_elem(void);
 
-/* Split-KV chunk from G4_ATTN_CHUNK (32, 64, 128, 256 or 512; unset -> 256 on MI355X). -1 if invalid.
+/* Split-KV chunk from G4_ATTN_CHUNK (32, 64, 128 or 256, the reference's set; unset -> 256 on MI355X, where the
+ * reference defaults to 64). -1 if invalid.
  * Replaces attn_split_chunk(), kernels/attention_decode_split.cuh:26-37. */
 int dgx_attn_split_chunk(void);
 /* ceil(max_len / chunk). Replaces attn_split_ns_cap(), kernels/attention_decode_split.cuh:173. */
@@ -65,8 +66,9 @@ hipError_t dgx_attn_decode_split(const float *Q, const void *Kc, const void *Vc,
 
 /* Flash attention over a KV cache: Sq query tokens at positions base .. base+Sq-1, causal, optional sliding
  * window, optional tree mask anc[Sq] (key j >= base attended iff bit j-base of anc[q], j-base < 32).
- * Its scratch grows inside the call when needed (as the reference's does); pre-size it with
- * dgx_flash_attn_reserve before graph capture.
+ * Runs of up to 32 tokens and every tree-masked run take the split kernel; a tree run of more than 32 tokens
+ * never attends nodes at bit 32 and beyond, as in the reference. Its scratch grows inside the call when needed
+ * (as the reference's does); pre-size it with dgx_flash_attn_reserve / _reserve_partials before graph capture.
  * Replaces launch_flash_attn<KV>() / launch_flash_attn2bs<HD,BC,NW,KV>(), kernels/attention_flash.cuh:273-306. */
 hipError_t dgx_flash_attn(const float *Q, const void *Kc, const void *Vc, int kv_dtype, float *O, float *lse,
                           int Sq, int NQ, int NKV, int HD, int base, hipStream_t st, const unsigned *anc,
@@ -84,6 +86,9 @@ hipError_t dgx_flash_attn_v2(const float *Q, const void *Kc, const void *Vc, int
                              int Sq, int NQ, int NKV, int HD, int base, hipStream_t st, float scale, int window,
                              int f16_mma);
 
+/* fp32 launchers below never allocate. They run the fp32 MFMA kernel (HD 128/256, up to 16 rows per KV head)
+ * when the flash scratch already holds its partials - rows * NQ * (max_pos / 512 + 1) of them, reserved with
+ * dgx_flash_attn_reserve_partials (or grown by an earlier flash call) - and the scalar fp32 kernels otherwise. */
 /* fp32 causal prefill over fp32 K/V [S, NKV, HD] (no S <= HD limit). Replaces launch_attn(), attention.cuh:72-79. */
 hipError_t dgx_attn(const float *Q, const float *K, const float *V, float *O, int S, int NQ, int NKV, int HD,
                     hipStream_t st, float scale, int window);

@@ -62,8 +62,9 @@ def test_kv_dtype_and_chunk_knobs(tmp_path):
     v, err = _knobs({"G4_KV_DTYPE": "fp8"})
     assert v[0] == -1 and "Invalid G4_KV_DTYPE" in err
     assert _knobs({"G4_ATTN_CHUNK": "64"})[0][1:3] == [64, 16]
-    v, err = _knobs({"G4_ATTN_CHUNK": "100"})
-    assert v[1] == -1 and "Invalid G4_ATTN_CHUNK" in err
+    for bad in ("100", "512"):                                      # the reference's set is 32/64/128/256
+        v, err = _knobs({"G4_ATTN_CHUNK": bad})
+        assert v[1] == -1 and "Invalid G4_ATTN_CHUNK" in err
     recipe = tmp_path / "recipe.env"
     recipe.write_text("# recipe\nG4_KV_DTYPE = bf16  # comment\nG4_ATTN_CHUNK=128\n")
     assert _knobs({"DGX_KNOBS_FILE": str(recipe)})[0][:2] == [2, 128]
