@@ -111,6 +111,33 @@ hipError_t pool_for(Pool *pools, Pool *&out) {
     return hipSuccess;
 }
 
+// ---------------------------------------------------------------- fixed scratch (allocation-free entry point)
+// dgx_attn_batch_noalloc keeps its split partials in this file-scope device array instead of a pool. Every GPU the
+// library runs on holds its own copy (kScratchBytes) until the process ends. Host code never passes the array's
+// name to a kernel: it is a host-side stand-in there. The device address comes from hipGetSymbolAddress, once per
+// device with that device current, and is kept in g_scratch_dev.
+constexpr size_t kScratchBytes = 64ull << 20;
+__device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+float *g_scratch_dev[kMaxDev];
+std::mutex g_scratch_mu;
+
+hipError_t scratch_ptr(float *&out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!ptr) return hipErrorInvalidSymbol;
+        g_scratch_dev[dev] = static_cast<float *>(ptr);
+    }
+    out = g_scratch_dev[dev];
+    return hipSuccess;
+}
+
 // A ring-buffer cache of kv_cap rows holds the sliding window of every row of a launch: the keys a launch reads
 // span at most window + T - 1 positions, and whole 64-key steps map to consecutive rows.
 bool ring_ok(int kv_cap, int window, int T) {
@@ -408,6 +435,36 @@ hipError_t dgx_attn_batch(const void *Q, int q_dtype, const void *Kc, const void
     const Problem p = make_problem(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, B, Tq, NQ, NKV, HD, kv_stride, 1, base,
                                    1, base_b, anc, max_pos, scale, window);
     return run_split(p, C, *pool, ns, st);
+}
+
+hipError_t dgx_attn_batch_noalloc(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
+                                  int o_dtype, float *lse, int B, int Tq, int NQ, int NKV, int HD, const int *base_b,
+                                  int base, long kv_stride, const unsigned *anc, int max_pos, int chunk,
+                                  hipStream_t st, float scale, int window) {
+    if (B == 0 || Tq == 0) return hipSuccess;
+    if (!Q || !Kc || !Vc || !O || B < 0 || Tq < 0 || NQ <= 0 || NKV <= 0 || NQ % NKV || !valid_hd(HD) || max_pos < 0 ||
+        !valid_dtype(q_dtype) || !valid_dtype(o_dtype) || kv_dtype == DT_FP32 || !valid_dtype(kv_dtype))
+        return hipErrorInvalidValue;
+    if (B > 1 && kv_stride == 0 && !base_b) return hipErrorInvalidValue;
+    const int C = chunk > 0 ? chunk : dgx_attn_split_chunk();
+    if (C <= 0 || C % 32) return hipErrorInvalidValue;
+    // Partials m [P], l [P] (each rounded up to 64 floats = 256 bytes) and acc [P * HD] in the fixed array.
+    const int ns = max_pos / C + 1;
+    const size_t P = (size_t)B * Tq * NQ * ns, Pa = (P + 63) / 64 * 64;
+    if (P > kScratchBytes / sizeof(float) || (2 * Pa + P * (size_t)HD) * sizeof(float) > kScratchBytes) {
+        fprintf(stderr, "[attn_batch_noalloc] %zu partials x (HD %d + 2) floats exceed the fixed %zu-byte scratch\n",
+                P, HD, kScratchBytes);
+        return hipErrorInvalidValue;
+    }
+    float *base_ptr = nullptr;
+    hipError_t e = scratch_ptr(base_ptr);
+    if (e != hipSuccess) return e;
+    Pool fixed;
+    fixed.m = base_ptr; fixed.l = base_ptr + Pa; fixed.acc = base_ptr + 2 * Pa;
+    fixed.cap = P; fixed.acc_cap = P * (size_t)HD;
+    const Problem p = make_problem(Q, q_dtype, Kc, Vc, kv_dtype, O, o_dtype, lse, B, Tq, NQ, NKV, HD, kv_stride, 1, base,
+                                   1, base_b, anc, max_pos, scale, window);
+    return run_split(p, C, fixed, ns, st);
 }
 
 hipError_t dgx_attn_batch_ex(const void *Q, int q_dtype, const void *Kc, const void *Vc, const void *const *Kp,

@@ -44,6 +44,7 @@ def lib():
             "dgx_kv_stats": ([P], I),
             "dgx_kv_append": ([P, P, P, P, I, I, I, L64, I, P, I, P], I),
             "dgx_attn_batch": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, P, I, I, P, F, I], I),
+            "dgx_attn_batch_noalloc": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, P, I, I, P, F, I], I),
             "dgx_attn_batch_ex": ([P, I, P, P, P, P, I, P, I, P, P, I, I, I, I, I, I, P, I, L64, P, I, I, P, F, I, I], I),
             "dgx_attn_prefill_ex": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, I, I, P, F, I, I], I),
             "dgx_attn_prefill": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, I, I, P, F, I], I),
@@ -154,6 +155,14 @@ def attn_batch(Q, K, V, O, B, Tq, NQ, NKV, HD, base_b, kv_stride, max_pos, chunk
     _ck(lib().dgx_attn_batch(_ptr(Q), _DT[Q.dtype], _ptr(K), _ptr(V), kv_code(K), _ptr(O), _DT[O.dtype], _ptr(lse),
                              B, Tq, NQ, NKV, HD, _ptr(base_b), base, kv_stride, _ptr(anc), max_pos, chunk, _stream(),
                              float(scale), window), "dgx_attn_batch")
+
+
+def attn_batch_noalloc(Q, K, V, O, B, Tq, NQ, NKV, HD, base_b, kv_stride, max_pos, chunk=0, anc=None, base=0,
+                       scale=0.0, window=0, lse=None):
+    """dgx_attn_batch_noalloc: dgx_attn_batch with its partials in the library's fixed device array."""
+    _ck(lib().dgx_attn_batch_noalloc(_ptr(Q), _DT[Q.dtype], _ptr(K), _ptr(V), kv_code(K), _ptr(O), _DT[O.dtype],
+                                     _ptr(lse), B, Tq, NQ, NKV, HD, _ptr(base_b), base, kv_stride, _ptr(anc), max_pos,
+                                     chunk, _stream(), float(scale), window), "dgx_attn_batch_noalloc")
 
 
 def attn_batch_ex(Q, O, B, Tq, NQ, NKV, HD, base_b, max_pos, K=None, V=None, kv_stride=0, Kp=None, Vp=None,

@@ -128,6 +128,17 @@ hipError_t dgx_attn_batch(const void *Q, int q_dtype, const void *Kc, const void
                           int o_dtype, float *lse, int B, int Tq, int NQ, int NKV, int HD, const int *base_b, int base,
                           long kv_stride, const unsigned *anc, int max_pos, int chunk, hipStream_t st, float scale,
                           int window);
+/* dgx_attn_batch that allocates nothing, for callers that cannot call hipMalloc (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation). No counterpart in the reference. Same arguments, rows
+ * and results as dgx_attn_batch (bit-identical: the same kernels), but the split partials live in a fixed 64 MiB
+ * device array inside the library (one per GPU, held until the process ends) instead of the reserved pool, so no
+ * dgx_attn_split_reserve is needed. Limit: B * Tq * NQ * (max_pos / chunk + 1) partials of (HD + 2) floats must
+ * fit in 64 MiB (e.g. BASELINE config 2 at chunk 512 needs 6.3 MB); larger calls return hipErrorInvalidValue.
+ * Calls that overlap on one GPU (different streams or host threads) share the array and race; serialize them. */
+hipError_t dgx_attn_batch_noalloc(const void *Q, int q_dtype, const void *Kc, const void *Vc, int kv_dtype, void *O,
+                                  int o_dtype, float *lse, int B, int Tq, int NQ, int NKV, int HD, const int *base_b,
+                                  int base, long kv_stride, const unsigned *anc, int max_pos, int chunk,
+                                  hipStream_t st, float scale, int window);
 /* dgx_attn_batch with two caller-side fusions for the Qwen callers (models/qwen35_batch.cu:165-167,333-335 and
  * models/qwen35_decode.cu:165-166):
  *   - Kp / Vp: device arrays of B per-slot K / V base pointers (each [max_len, NKV, HD]); when given they replace
