@@ -140,6 +140,7 @@ __device__ __forceinline__ f32x4 mfma16k16(const u32x2 &a, const u32x2 &b, const
         return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
 }
 
+
 // LDS transpose read (gfx950 ds_read_b64_tr_b16). Within each 16-lane group g, lane i passes the address of
 // row 4g + i/4, columns 4*(i%4)..+3 of a row-major 16-bit tile; lane n of the group receives column n of
 // rows 4g..4g+3. With rows = keys and columns = head dims this is the A fragment of O^T += V^T P^T for a
@@ -149,6 +150,22 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t *p) {
     const lds_s4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (__attribute__((address_space(3))) lds_s4 *)(reinterpret_cast<uintptr_t>(p)));
     return __builtin_bit_cast(u32x2, r);
+}
+
+// Buffer resource of a raw byte range [base, base + bytes) (no stride, no swizzle): buffer loads at vector
+// offsets past `bytes` return zeros instead of touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    // wave-uniform operands (readfirstlane), so the resource lives in SGPRs and no waterfall loop is generated
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a) |
+                       ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) << 32);
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(u), (short)0,
+                                             __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000);
+}
+// 16 bytes per lane from buffer offset voffset into LDS at lds + 16 * lane (gfx950 buffer_load_dwordx4 ... lds).
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, void *lds, int voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(reinterpret_cast<uintptr_t>(lds)),
+                                             16, voffset, 0, 0, 0);
 }
 
 // Online-softmax rescale threshold (log2 units): the running reference max of a row moves only when a new score

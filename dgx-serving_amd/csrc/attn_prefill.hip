@@ -33,6 +33,7 @@
 // (attention_flash.cuh:177), and such short query runs go to the split kernel.
 #include "attn_device.h"
 #include "attn_internal.h"
+#include <algorithm>
 #include <climits>
 #include <type_traits>
 
@@ -49,35 +50,50 @@ struct PrefArgs {
     int nitems;        // work items per (sequence, kv head)
     int nwg;           // total work items
     float sl2;         // scale * log2(e)
+    int fold;          // 1: fold each XCD's slots (two co-resident workgroups per CU take a long and a short item)
 };
 
-// A workgroup is RG x KG waves. RB: 16-row blocks per wave; RG: row groups (waves splitting the tile's rows, the
-// first half of them on the first half tile); KG: key groups (waves splitting each step's keys); NS: LDS stages;
-// NSUB: 16-key sub-tiles per wave and step.
-template <int HD, int RB, int RG, int KG_, int NS_, int NSUB_>
+// A workgroup is RG x KG waves. RB: 16-row blocks per wave; RG: row groups (waves splitting the tile's rows); KG:
+// key groups (waves splitting each step's keys); NS: LDS stages; NSUB: 16-key sub-tiles per wave and step.
+// MIX = false: RB = 1, the row groups split the tile's rows (the first half of them on the first half tile).
+// MIX = true: RB = 2, row group rg holds rows [16 rg, 16 rg + 16) of BOTH half tiles (block 0 from the first,
+// block 1 from the second), so in a causal pair every wave works while either half has keys, and a K or V
+// fragment read from LDS serves both blocks.
+template <int HD, int RB, int RG, int KG_, int NS_, int NSUB_, bool MIX_>
 struct PrefCfg {
     static constexpr int KG = KG_, NS = NS_, NW = RG * KG_, NT = NW * 64, NSUB = NSUB_;
+    static constexpr bool MIX = MIX_;
     static constexpr int KT = 16 * NSUB;                 // keys per wave per step (NSUB 16-key sub-tiles)
     static constexpr int SK = KG * KT;                   // keys per step
     static constexpr int RR = RG * RB * 16;              // rows per workgroup tile
     static constexpr int HR = RR / 2;                    // rows per half tile
     static constexpr int KS = HD / 32;                   // QK k-steps (16x16x32)
     static constexpr int DB = HD / 16;                   // PV output dim blocks (16x16x16)
+    static constexpr int DO = DB / KG;                   // output dim blocks each key group finishes
     static constexpr int SLOTS = HD / 8;                 // 16-byte slots per key row
     static constexpr int ROWB = HD * 2;                  // bytes per key row (16-bit operands)
     static constexpr int HALF = SK * ROWB;               // bytes of one K (or V) step tile
     static constexpr int STAGE = 2 * HALF;               // K and V of one step
     static constexpr int NLD = SK * SLOTS / NT;          // 16-byte loads per thread per step (K and V each)
     static constexpr size_t LDS_TILES = (size_t)NS * STAGE;
-    static constexpr int XSTR = HD / 2 + 4;              // merge exchange row stride (floats)
-    static constexpr size_t LDS_MERGE = (size_t)RG * 2 * RB * 16 * XSTR * 4;
+    static constexpr int XSTR = HD / KG + 4;             // merge exchange row stride (floats)
+    // merge exchange of one row block: [row group][owner key group][sender slot (KG-1)][16 rows][XSTR]
+    static constexpr size_t LDS_MERGE = (size_t)RG * KG * (KG - 1) * 16 * XSTR * 4;
     static constexpr size_t LDS_STATS = (size_t)2 * NW * RB * 16 * 4;
     static constexpr size_t LDS_MAIN = LDS_TILES > LDS_MERGE ? LDS_TILES : LDS_MERGE;
-    static constexpr size_t LDS = LDS_MAIN + LDS_STATS;
+    // MIX: the Q fragments of both blocks sit in LDS in fragment order [block][row group][k-step][lane] (16 B
+    // each), which keeps the wave within 256 VGPRs (two waves per SIMD); the merge statistics then use the tile
+    // region past the merge exchange (both are needed only after the step loop).
+    static constexpr int QR = MIX ? 0 : RB;              // row blocks whose Q fragments stay in registers
+    static constexpr size_t LDS_Q = MIX ? (size_t)RB * RG * KS * 1024 : 0;
+    static constexpr bool STATS_IN_MAIN = MIX && LDS_MERGE + LDS_STATS <= LDS_MAIN;
+    static constexpr size_t STATS_OFF = STATS_IN_MAIN ? LDS_MERGE : LDS_MAIN;
+    static constexpr size_t LDS = LDS_MAIN + (STATS_IN_MAIN ? 0 : LDS_STATS) + LDS_Q;
+    static constexpr size_t Q_OFF = LDS - LDS_Q;
     static_assert(NLD >= 1 && (SK * SLOTS) % NT == 0, "step loads");
-    static_assert(RG % 2 == 0 && HR % (RB * 16) == 0, "each wave's rows lie in one half tile");
+    static_assert(MIX ? RB == 2 : (RB == 1 && RG % 2 == 0), "row block layout");
     static_assert(NS >= 2 && NS <= 4, "stages");
-    static_assert(KG == 2, "the merge pairs two key groups");
+    static_assert((KG == 2 || KG == 4) && DB % KG == 0, "key groups");
 };
 
 // Slot swizzle of key row k: 16-byte column c of key k sits in slot c ^ swz(k), a permutation of the low 4 key
@@ -97,22 +113,26 @@ __device__ __forceinline__ void wait_steps(int pending) {
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <int HD, int RB, int RG, int KG_, int NS_, int NSUB, int KVT, int QT, int OT>
-__global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a) {
-    using Cf = PrefCfg<HD, RB, RG, KG_, NS_, NSUB>;
-    constexpr int KG = Cf::KG, NS = Cf::NS, SK = Cf::SK, KS = Cf::KS, DB = Cf::DB, NLD = Cf::NLD;
+template <int HD, int RB, int RG, int KG_, int NS_, int NSUB, bool MIX, int WPE, int KVT, int QT, int OT>
+__global__ void __launch_bounds__(RG * KG_ * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
+prefill_kernel(const PrefArgs a) {
+    using Cf = PrefCfg<HD, RB, RG, KG_, NS_, NSUB, MIX>;
+    constexpr int KG = Cf::KG, NS = Cf::NS, SK = Cf::SK, KS = Cf::KS, DB = Cf::DB, NLD = Cf::NLD, DO = Cf::DO;
     constexpr int SLOTS = Cf::SLOTS, ROWB = Cf::ROWB, HR = Cf::HR;
     constexpr bool F16 = OpIsF16<KVT>::value;
     constexpr bool DMA = KVT != DT_FP32;                 // 16-bit caches go straight to LDS
     using KE = typename Elem<KVT>::T;
     using QE = typename Elem<QT>::T;
     extern __shared__ __align__(16) unsigned char smem[];
-    float *stm = reinterpret_cast<float *>(smem + Cf::LDS_MAIN), *stl = stm + Cf::NW * RB * 16;
+    float *stm = reinterpret_cast<float *>(smem + Cf::STATS_OFF), *stl = stm + Cf::NW * RB * 16;
 
     const Problem &p = a.p;
-    // XCD-aware work index: dispatch slot b runs on XCD b % 8; consecutive work items share an XCD.
-    const int per = (int)gridDim.x / 8;
-    const int w_item = ((int)blockIdx.x % 8) * per + (int)blockIdx.x / 8;
+    // XCD-aware work index: dispatch slot b runs on XCD b % 8, and consecutive work items (one KV head's tiles,
+    // longest first) share an XCD, so that head's K/V stays in one L2. With a.fold the local slot k is folded:
+    // slots k and k + per/2 - which the dispatcher places on the same CU when two workgroups fit a CU and the grid
+    // is one round - take the k-th longest and the k-th shortest item.
+    const int per = (int)gridDim.x / 8, k_loc = (int)blockIdx.x / 8, h_loc = (per + 1) / 2;
+    const int w_item = ((int)blockIdx.x % 8) * per + (!a.fold || k_loc < h_loc ? k_loc : per - 1 - (k_loc - h_loc));
     if (w_item >= a.nwg) return;
     const int seq = w_item / (p.NKV * a.nitems);
     const int kvh = (w_item / a.nitems) % p.NKV;
@@ -156,61 +176,103 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
     }
     // Step k of the walk into stage k % NS. Keys past the last position re-read that position (they are masked), so
     // every load is in bounds; only a step that crosses the end needs the clamped addresses.
-    auto issue = [&](int k) {
-        const int s = s0 + k;
-        unsigned char *kd = smem + (size_t)(k % NS) * Cf::STAGE, *vd = kd + Cf::HALF;
-        const char *ks = reinterpret_cast<const char *>(Kb) + (size_t)key_row(p, s * SK) * krow_b;
-        const char *vs = reinterpret_cast<const char *>(Vb) + (size_t)key_row(p, s * SK) * krow_b;
-        const bool inside = s * SK + SK <= hi_b;
+    // Loads [u0, u1) of the thread's NLD slots (K and V each).
+    // 16-bit caches: buffer loads straight into LDS over the byte range the workgroup may read (the ring, or the
+    // keys below hi_b), so the rows past the last key of a step read as zeros (they are masked) without clamping.
+    const uint32_t kv_bytes = p.kv_cap > 0 ? (uint32_t)p.kv_cap * krow_b
+                                           : (uint32_t)(max(hi_b, 1) - 1) * krow_b + (uint32_t)(HD * sizeof(KE));
+    int it_cur = 0;                                                     // the step being computed
+    // Step k < 0 is a no-op step: every lane is out of range, so its loads write zeros into the stage of the step
+    // before (already consumed by every wave) and touch no memory; this keeps the issue points branch-free.
+    auto issue_part = [&](int k, int u0, int u1) {
+        const int s = s0 + (k < 0 ? 0 : k);
+        unsigned char *kd = smem + (size_t)((k < 0 ? it_cur + 1 : k) % NS) * Cf::STAGE, *vd = kd + Cf::HALF;
+        const int soff = __builtin_amdgcn_readfirstlane(key_row(p, s * SK) * (int)krow_b);
+        // the step's rows as the buffer (the range check covers the vector offset only)
+        const uint32_t left = k < 0 || (uint32_t)soff >= kv_bytes ? 0u : kv_bytes - (uint32_t)soff;
+        const __amdgpu_buffer_rsrc_t krs = make_rsrc(reinterpret_cast<const char *>(Kb) + soff, left);
+        const __amdgpu_buffer_rsrc_t vrs = make_rsrc(reinterpret_cast<const char *>(Vb) + soff, left);
 #pragma unroll
         for (int u = 0; u < NLD; u++) {
+            if (u < u0 || u >= u1) continue;
             const int i = wave * NLD + u;
-            unsigned off = ld_off[u];
-            if (!inside) {
-                const unsigned key = off / krow_b, lim = (unsigned)(hi_b - 1 - s * SK);
-                if (key > lim) off -= (key - lim) * krow_b;
-            }
             if constexpr (!DMA) {
+                const char *ks = reinterpret_cast<const char *>(Kb) + soff;
+                const char *vs = reinterpret_cast<const char *>(Vb) + soff;
+                unsigned off = ld_off[u];
+                if (s * SK + SK > hi_b) {
+                    const unsigned key = off / krow_b, lim = (unsigned)(hi_b - 1 - s * SK);
+                    if (key > lim) off -= (key - lim) * krow_b;
+                }
                 const int S = i * 64 + lane;
                 *reinterpret_cast<u32x4 *>(kd + (size_t)S * 16) = load8_op<KVT, F16>(reinterpret_cast<const KE *>(ks + off));
                 *reinterpret_cast<u32x4 *>(vd + (size_t)S * 16) = load8_op<KVT, F16>(reinterpret_cast<const KE *>(vs + off));
             } else {
-                __builtin_amdgcn_global_load_lds((glb_void *)(ks + off), (lds_void *)(kd + (size_t)i * 1024), 16, 0, 0);
-                __builtin_amdgcn_global_load_lds((glb_void *)(vs + off), (lds_void *)(vd + (size_t)i * 1024), 16, 0, 0);
+                buffer_load_lds16(krs, kd + (size_t)i * 1024, (int)ld_off[u]);
+                buffer_load_lds16(vrs, vd + (size_t)i * 1024, (int)ld_off[u]);
             }
         }
     };
+    auto issue = [&](int k) { issue_part(k, 0, NLD); };
+    // The next step's loads go out in four parts spread over the current step (between the QK batches, after
+    // the softmax, between the PV batches): a workgroup's 8 waves issuing all of them at once stalled every wave
+    // on the vector memory pipe for about a thousand cycles per step.
+    constexpr int NPART = 4, PPART = (NLD + NPART - 1) / NPART;
+    auto issue_pt = [&](int k, int pt) { issue_part(k, pt * PPART, min(NLD, (pt + 1) * PPART)); };
     if (nsteps > 0) issue(0);
 
-    // This wave's rows (all in one half tile): Q fragments and positions (an invalid row has pos = -1 and attends
-    // nothing), and the wave-uniform key span of its rows (positions grow with the row's token).
-    const int half = (rg * RB * 16) / HR, lr0 = rg * RB * 16 - half * HR;
-    const int htok0 = half ? tok0[1] : tok0[0], hnrows = (half ? tok1[1] - tok0[1] : tok1[0] - tok0[0]) * GRP;
-    int rpos[RB], rlo[RB];
-    u32x4 qop[RB][KS];
+    // This wave's row blocks: block rb covers rows [lrow[rb], lrow[rb] + 16) of half tile hb[rb]. Q fragments and
+    // positions per row (an invalid row has pos = -1 and attends nothing), and the wave-uniform key span of each
+    // block (positions grow with the row's token).
+    int htok[RB], hrows[RB], lrow[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
-        const int rho = lr0 + rb * 16 + ln;
-        const bool valid = rho < hnrows;
-        const int t = htok0 + (valid ? rho / GRP : 0), h = kvh * GRP + (valid ? rho % GRP : 0);
+        const int hb = MIX ? rb : (rg * 16) / HR;
+        lrow[rb] = MIX ? rg * 16 : rg * 16 - hb * HR;
+        htok[rb] = hb ? tok0[1] : tok0[0];
+        hrows[rb] = (hb ? tok1[1] - tok0[1] : tok1[0] - tok0[0]) * GRP;
+    }
+    int rpos[RB], rlo[RB];
+    constexpr int QR = Cf::QR;
+    u32x4 qop[QR > 0 ? QR : 1][KS];
+    unsigned char *qlds = smem + Cf::Q_OFF;                             // MIX: Q fragments [rb][rg][ks][lane]
+    const unsigned qaddr = (unsigned)(uintptr_t)qlds + (unsigned)(rg * KS * 1024 + lane * 16);
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+        const int rho = lrow[rb] + ln;
+        const bool valid = rho < hrows[rb];
+        const int t = htok[rb] + (valid ? rho / GRP : 0), h = kvh * GRP + (valid ? rho % GRP : 0);
         const int ps = pbase + t;
         rpos[rb] = valid ? ps : -1;
         rlo[rb] = win_lo(ps, p.window);
         const QE *qrow = reinterpret_cast<const QE *>(p.Q) + ((size_t)(seq * p.T + t) * p.NQ + h) * HD + 8 * g;
+        if (rb < QR) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++)
-            qop[rb][ks] = valid ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
+            for (int ks = 0; ks < KS; ks++)
+                qop[rb < QR ? rb : 0][ks] = valid ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
+        } else if (kg == 0) {                                           // one wave per row group stores them
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+                *reinterpret_cast<u32x4 *>(qlds + (size_t)((rb * RG + rg) * KS + ks) * 1024 + lane * 16) =
+                    valid ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
+        }
     }
     // Steps 1..NS-2 go out after the Q loads, so that waiting for step it never waits for younger steps.
 #pragma unroll
     for (int k = 1; k < NS - 1; k++)
         if (k < nsteps) issue(k);
-    const int rho1 = min(hnrows, lr0 + RB * 16);
-    int wlo = INT_MAX, whi = -1, lo_max = 0, pos_min = INT_MAX;
-    if (lr0 < rho1) {
-        const int pf = pbase + htok0 + lr0 / GRP, pl = pbase + htok0 + (rho1 - 1) / GRP;
-        wlo = max(win_lo(pf, p.window), j_lo); whi = min(pl, j_hi - 1);
-        lo_max = win_lo(pl, p.window); pos_min = pf;
+    int wlo[RB], whi[RB], lo_max[RB], pos_min[RB];
+    int wlo_all = INT_MAX, whi_all = -1;
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+        const int rho1 = min(hrows[rb], lrow[rb] + 16);
+        wlo[rb] = INT_MAX; whi[rb] = -1; lo_max[rb] = 0; pos_min[rb] = INT_MAX;
+        if (lrow[rb] < rho1) {
+            const int pf = pbase + htok[rb] + lrow[rb] / GRP, pl = pbase + htok[rb] + (rho1 - 1) / GRP;
+            wlo[rb] = max(win_lo(pf, p.window), j_lo); whi[rb] = min(pl, j_hi - 1);
+            lo_max[rb] = win_lo(pl, p.window); pos_min[rb] = pf;
+        }
+        wlo_all = min(wlo_all, wlo[rb]); whi_all = max(whi_all, whi[rb]);
     }
 
     float m[RB], l[RB];
@@ -230,42 +292,108 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
     const int vr = 4 * g + (ln >> 2);
     const unsigned kaddr = lds0 + (kg * Cf::KT + ln) * ROWB + ((g ^ swz(ln)) << 4);
     const unsigned vaddr = lds0 + Cf::HALF + (kg * Cf::KT + vr) * ROWB + 8 * (ln & 1) + ((((ln & 3) >> 1) ^ swz(vr)) << 4);
-    for (int it = 0; it < nsteps; it++) {
-        // Step it is the oldest load batch in flight; up to NS-2 younger steps may stay in flight.
-        wait_steps<DMA ? 2 * NLD : 0>(min(NS - 2, nsteps - 1 - it));
-        __syncthreads();                                                // everyone's step it, and step it-1 is consumed
-        if (it + NS - 1 < nsteps) issue(it + NS - 1);
-        // This wave's keys of the step: NSUB 16-key sub-tiles from jw. QK for all of them first (independent MFMA
-        // chains), one softmax update over all of them, then PV.
-        const int jw = (s0 + it) * SK + kg * Cf::KT;
-        if (jw > whi || jw + Cf::KT - 1 < wlo) continue;                // no row of the wave attends them
-        const unsigned stage = (it % NS) * Cf::STAGE;
+
+    // One step's work for the row blocks in ACT (a wave-uniform bit mask). QK: the K fragments of a sub-tile are
+    // read in batches of 4 k-steps (inline asm, one wait per batch, so the reads are not serialised behind the
+    // MFMAs) and each active row block runs its MFMA chain on them. Then one softmax update, then PV with V^T
+    // fragments in batches of 8 transpose reads. A block left out keeps its state exactly (it attends no key).
+    auto step = [&](const int ACT, int jw, unsigned stage, int nxt) {
+        int pt = 0;
+        // Per-lane LDS bases, made opaque so that the XOR-swizzled fragment addresses are formed next to their
+        // reads instead of being hoisted out of the step loop (which held ~30 address registers live and spilled).
+        unsigned kbase = kaddr + stage, vbase = vaddr + stage, qbase = qaddr;
+        asm volatile("" : "+v"(kbase), "+v"(vbase), "+v"(qbase));
         f32x4 s[NSUB][RB], s2[NSUB][RB];
 #pragma unroll
         for (int sub = 0; sub < NSUB; sub++)
 #pragma unroll
             for (int rb = 0; rb < RB; rb++) s[sub][rb] = s2[sub][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (!MIX) {
+            // Software-pipelined: batch b = k-steps 2b, 2b+1 of every sub-tile (4 reads at NSUB = 2); batch b+1 is
+            // read before batch b's MFMAs, so the LDS latency hides under them (4 independent MFMA chains).
+            constexpr int KPB = 2, NB = KS / KPB, RPB = KPB * NSUB;
+            static_assert(RPB == 4 || RPB == 2, "batch size");
+            u32x4 kb[2][RPB];
+            auto rd = [&](int b, u32x4 (&dst)[RPB]) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
+                for (int sub = 0; sub < NSUB; sub++)
+#pragma unroll
+                    for (int kk = 0; kk < KPB; kk++)
+                        asm volatile("ds_read_b128 %0, %1" : "=v"(dst[sub * KPB + kk])
+                                     : "v"((kbase + sub * 16 * ROWB) ^ (64u * (b * KPB + kk))) : "memory");
+            };
+            rd(0, kb[0]);
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                u32x4 (&cur)[RPB] = kb[b & 1];
+                if (b + 1 < NB) {
+                    rd(b + 1, kb[(b + 1) & 1]);
+                    if constexpr (RPB == 4)
+                        asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3])::"memory");
+                    else
+                        asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(cur[0]), "+v"(cur[RPB - 1])::"memory");
+                } else {
+                    if constexpr (RPB == 4)
+                        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3])::"memory");
+                    else
+                        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(cur[0]), "+v"(cur[RPB - 1])::"memory");
+                }
+                if (b == 0 || b == NB / 2) issue_pt(nxt, pt++);
+#pragma unroll
+                for (int sub = 0; sub < NSUB; sub++)
+#pragma unroll
+                    for (int kk = 0; kk < KPB; kk++) {
+                        if (kk & 1) s2[sub][0] = mfma16<F16>(cur[sub * KPB + kk], qop[0][b * KPB + kk], s2[sub][0]);
+                        else s[sub][0] = mfma16<F16>(cur[sub * KPB + kk], qop[0][b * KPB + kk], s[sub][0]);
+                    }
+            }
+        }
+        if constexpr (MIX) {
+            // Batches of 2 k-steps: the K fragments of the sub-tile and the Q fragments of each active block (Q
+            // from LDS at constant offsets from one base). Small batches keep the wave within 256 VGPRs; the second
+            // wave on the SIMD covers the read latency.
 #pragma unroll
             for (int sub = 0; sub < NSUB; sub++) {
-                const u32x4 kf = *reinterpret_cast<const u32x4 *>(smem + ((kaddr + stage + sub * 16 * ROWB) ^ (64u * ks)) - lds0);
+                const unsigned ka = kbase + sub * 16 * ROWB;
 #pragma unroll
-                for (int rb = 0; rb < RB; rb++) {
-                    if (ks & 1) s2[sub][rb] = mfma16<F16>(kf, qop[rb][ks], s2[sub][rb]);
-                    else s[sub][rb] = mfma16<F16>(kf, qop[rb][ks], s[sub][rb]);
+                for (int k2 = 0; k2 < KS; k2 += 2) {
+                    u32x4 kf[2], qf[2][2];
+#pragma unroll
+                    for (int q = 0; q < 2; q++)
+                        asm volatile("ds_read_b128 %0, %1" : "=v"(kf[q]) : "v"(ka ^ (64u * (k2 + q))) : "memory");
+#pragma unroll
+                    for (int rb = 0; rb < RB; rb++) {
+                        if ((ACT >> rb) & 1) {
+#pragma unroll
+                            for (int q = 0; q < 2; q++)
+                                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(qf[rb][q])
+                                             : "v"(qbase), "n"(1024 * ((rb * RG) * KS + k2 + q)) : "memory");
+                        }
+                    }
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kf[0]), "+v"(kf[1]), "+v"(qf[0][0]), "+v"(qf[0][1]),
+                                 "+v"(qf[1][0]), "+v"(qf[1][1])::"memory");
+                    if (k2 == 0 || k2 == KS / 2) issue_pt(nxt, pt++);
+#pragma unroll
+                    for (int rb = 0; rb < RB; rb++) {
+                        if ((ACT >> rb) & 1) {
+#pragma unroll
+                            for (int q = 0; q < 2; q++) s[sub][rb] = mfma16<F16>(kf[q], qf[rb][q], s[sub][rb]);
+                        }
+                    }
                 }
             }
         }
-        const bool full = jw >= j_lo && jw + Cf::KT <= j_hi && jw >= lo_max && jw + Cf::KT - 1 <= pos_min;
         float tv[NSUB][RB][4], mnew[RB];
         bool need = false;
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
+            mnew[rb] = m[rb];
+            if (!((ACT >> rb) & 1)) continue;
+            const bool full = jw >= j_lo && jw + Cf::KT <= j_hi && jw >= lo_max[rb] && jw + Cf::KT - 1 <= pos_min[rb];
             float mx = kNegInf;
 #pragma unroll
             for (int sub = 0; sub < NSUB; sub++) {
-                const f32x4 sc = (s[sub][rb] + s2[sub][rb]) * a.sl2;
+                const f32x4 sc = (RB == 1 ? s[sub][rb] + s2[sub][rb] : s[sub][rb]) * a.sl2;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int key = jw + 16 * sub + 4 * g + i;
@@ -275,9 +403,11 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
                 }
             }
             mx = max_over_groups(mx);
-            if (mx > m[rb] + kRescaleThreshold) { mnew[rb] = mx; need = true; } else mnew[rb] = m[rb];
+            if (mx > m[rb] + kRescaleThreshold) { mnew[rb] = mx; need = true; }
         }
         if (__any(need)) {
+            // every block (an inactive one has mnew == m, alpha = 1): a per-block condition here made the compiler
+            // keep two copies of the accumulator
 #pragma unroll
             for (int rb = 0; rb < RB; rb++) {
                 const float alpha = (mnew[rb] == m[rb]) ? 1.f : fast_exp2(m[rb] - mnew[rb]);
@@ -286,77 +416,146 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
                 for (int db = 0; db < DB; db++) acc[rb][db] *= alpha;
             }
         }
+        while (pt < 3) issue_pt(nxt, pt++);
         u32x2 pop[NSUB][RB];
 #pragma unroll
         for (int sub = 0; sub < NSUB; sub++)
 #pragma unroll
             for (int rb = 0; rb < RB; rb++) {
+                if (!((ACT >> rb) & 1)) { pop[sub][rb] = u32x2{0u, 0u}; continue; }
                 float pv[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) pv[i] = (tv[sub][rb][i] == kNegInf) ? 0.f : fast_exp2(tv[sub][rb][i] - m[rb]);
                 l[rb] += (pv[0] + pv[1]) + (pv[2] + pv[3]);
                 pop[sub][rb] = u32x2{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3])};
             }
-        // V^T fragments in batches of 8 transpose reads, then one wait: the reads are issued as inline asm so
-        // that the compiler does not order them behind the direct-to-LDS loads of later steps.
+        if constexpr (!MIX) {
+            // Software-pipelined PV: batch b = 8 dim blocks of one sub-tile; batch b+1 is read before batch b's MFMAs.
+            constexpr int PB = 8, NPB = NSUB * DB / PB;
+            u32x2 vb2[2][PB];
+            auto rdv = [&](int b, u32x2 (&dst)[PB]) {
+                const int sub = b / (DB / PB), d0 = (b % (DB / PB)) * PB;
 #pragma unroll
-        for (int sub = 0; sub < NSUB; sub++)
+                for (int j = 0; j < PB; j++)
+                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(dst[j]) : "v"((vbase + sub * 16 * ROWB) ^ (32u * (d0 + j))) : "memory");
+            };
+            rdv(0, vb2[0]);
 #pragma unroll
-            for (int d8 = 0; d8 < DB; d8 += 8) {
-                u32x2 v[8];
-                const unsigned va = vaddr + stage + sub * 16 * ROWB;
+            for (int b = 0; b < NPB; b++) {
+                u32x2 (&cur)[PB] = vb2[b & 1];
+                if (b + 1 < NPB) {
+                    rdv(b + 1, vb2[(b + 1) & 1]);
+                    asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]),
+                                 "+v"(cur[5]), "+v"(cur[6]), "+v"(cur[7])::"memory");
+                } else {
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]),
+                                 "+v"(cur[5]), "+v"(cur[6]), "+v"(cur[7])::"memory");
+                }
+                const int sub = b / (DB / PB), d0 = (b % (DB / PB)) * PB;
 #pragma unroll
-                for (int j = 0; j < 8; j++)
-                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v[j]) : "v"(va ^ (32u * (d8 + j))) : "memory");
-                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]),
-                             "+v"(v[5]), "+v"(v[6]), "+v"(v[7])::"memory");
-#pragma unroll
-                for (int j = 0; j < 8; j++)
-#pragma unroll
-                    for (int rb = 0; rb < RB; rb++) acc[rb][d8 + j] = mfma16k16<F16>(v[j], pop[sub][rb], acc[rb][d8 + j]);
+                for (int j = 0; j < PB; j++) acc[0][d0 + j] = mfma16k16<F16>(cur[j], pop[sub][0], acc[0][d0 + j]);
+                if (pt < NPART && b % 2 == 1) issue_pt(nxt, pt++);
             }
+        }
+        if constexpr (MIX) {
+            // Software-pipelined PV, double-buffered: batch b = 4 dim blocks of one sub-tile; batch b+1 is read
+            // before batch b's MFMAs.
+            constexpr int PB = 4, NPB = NSUB * DB / PB;
+            u32x2 vb4[2][PB];
+            auto rdv = [&](int b, u32x2 (&dst)[PB]) {
+                const int sub = b / (DB / PB), d0 = (b % (DB / PB)) * PB;
+#pragma unroll
+                for (int j = 0; j < PB; j++)
+                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(dst[j]) : "v"((vbase + sub * 16 * ROWB) ^ (32u * (d0 + j))) : "memory");
+            };
+            rdv(0, vb4[0]);
+#pragma unroll
+            for (int b = 0; b < NPB; b++) {
+                u32x2 (&cur)[PB] = vb4[b & 1];
+                if (b + 1 < NPB) {
+                    rdv(b + 1, vb4[(b + 1) & 1]);
+                    asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3])::"memory");
+                } else {
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3])::"memory");
+                }
+                const int sub = b / (DB / PB), d0 = (b % (DB / PB)) * PB;
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) {
+                    if ((ACT >> rb) & 1) {
+#pragma unroll
+                        for (int j = 0; j < PB; j++) acc[rb][d0 + j] = mfma16k16<F16>(cur[j], pop[sub][rb], acc[rb][d0 + j]);
+                    }
+                }
+                if (pt < NPART && b % 2 == 1) issue_pt(nxt, pt++);
+            }
+        }
+        while (pt < NPART) issue_pt(nxt, pt++);
+    };
+
+    // The wave's keys of step it start at jw(it) = (s0 + it) * SK + kg * KT. It attends steps [it0, it1]: before
+    // and after them it only keeps the barriers and the loads going. Three loops instead of a skip branch keep the
+    // step loop a single path (a skip path made the register allocator copy the accumulator on every step).
+    auto fdiv = [](int x, int y) { return x >= 0 ? x / y : -((-x + y - 1) / y); };
+    const int jb = s0 * SK + kg * Cf::KT;
+    const int it0 = __builtin_amdgcn_readfirstlane(max(0, -fdiv(-(wlo_all - Cf::KT + 1 - jb), SK)));
+    const int it1 = __builtin_amdgcn_readfirstlane(whi_all < 0 ? -1 : min(nsteps - 1, fdiv(whi_all - jb, SK)));
+    auto sync_step = [&](int it) {
+        // Step it is the oldest load batch in flight; up to NS-2 younger steps may stay in flight.
+        wait_steps<DMA ? 2 * NLD : 0>(min(NS - 2, nsteps - 1 - it));
+        __syncthreads();                                                // everyone's step it, and step it-1 is consumed
+        it_cur = it;
+        return it + NS - 1 < nsteps ? it + NS - 1 : -1;
+    };
+    int it = 0;
+    for (; it < min(it0, nsteps); it++) issue(sync_step(it));
+    for (; it <= it1; it++) {
+        const int nxt = sync_step(it);
+        const int jw = (s0 + it) * SK + kg * Cf::KT;
+        const unsigned stage = (it % NS) * Cf::STAGE;
+        int act = 0;                                                    // wave-uniform mask of active row blocks
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) act |= (jw > whi[rb] || jw + Cf::KT - 1 < wlo[rb]) ? 0 : 1 << rb;
+        step(RB == 1 ? 1 : __builtin_amdgcn_readfirstlane(act), jw, stage, nxt);
     }
+    for (; it < nsteps; it++) issue(sync_step(it));
+    // The no-op loads of the last steps still write (zeros) into a stage: drain them before the merge reuses the
+    // tile region for its exchange and statistics.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) l[rb] = sum_over_groups(l[rb]);
     __syncthreads();                                                 // every wave is done with the K/V tiles
 
-    // Merge the two key-group states of each row (waves kg = 0 and 1 of a row group hold the same rows). Every
-    // lane derives the row's M = max m and L = sum l 2^(m - M) from the published (m, l) and scales its
-    // accumulator by 2^(m - M) / L (2^(m - M) for a split partial). Wave kg then owns output dims
-    // [kg*HD/2, (kg+1)*HD/2): it parks the other half of its scaled accumulator in LDS for its partner, reads
-    // the partner's half for its own dims, adds (a + b == b + a, so both orders give the same bits) and stores.
+    // Merge the KG key-group states of each row (waves kg = 0..KG-1 of a row group hold the same rows). Every
+    // lane derives the row's M = max m and L = sum l 2^(m - M) (key groups in order) from the published (m, l)
+    // and scales its accumulator by 2^(m - M) / L (2^(m - M) for a split partial). Key group kg then owns output
+    // dim blocks [kg*DO, (kg+1)*DO): it parks the other groups' blocks of its scaled accumulator in LDS, and sums
+    // its own blocks over the key groups in order 0..KG-1 (the same order for every row and tiling).
     const int NQ = p.NQ;
     if (g == 0) {
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) { stm[wave * RB * 16 + rb * 16 + ln] = m[rb]; stl[wave * RB * 16 + rb * 16 + ln] = l[rb]; }
     }
     __syncthreads();
-    constexpr int DH = DB / 2;                                          // dim blocks per owner
-    float *xb = reinterpret_cast<float *>(smem);                        // [rg][owner kg][row][XSTR] (reuses tiles)
-    float fsc[RB];
+    float *xb = reinterpret_cast<float *>(smem);                        // exchange (reuses the tiles)
+    auto slot = [](int sender, int owner) { return sender < owner ? sender : sender - 1; };
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
         const int srow = rb * 16 + ln;
-        const float m0 = stm[(rg * 2) * RB * 16 + srow], m1 = stm[(rg * 2 + 1) * RB * 16 + srow];
-        const float M = fmaxf(m0, m1);
+        float M = kNegInf;
+#pragma unroll
+        for (int k = 0; k < KG; k++) M = fmaxf(M, stm[(rg * KG + k) * RB * 16 + srow]);
         float L = 0.f;
-        if (m0 != kNegInf) L += stl[(rg * 2) * RB * 16 + srow] * fast_exp2(m0 - M);
-        if (m1 != kNegInf) L += stl[(rg * 2 + 1) * RB * 16 + srow] * fast_exp2(m1 - M);
+#pragma unroll
+        for (int k = 0; k < KG; k++) {
+            const float mk = stm[(rg * KG + k) * RB * 16 + srow];
+            if (mk != kNegInf) L += stl[(rg * KG + k) * RB * 16 + srow] * fast_exp2(mk - M);
+        }
         float f = (m[rb] == kNegInf) ? 0.f : fast_exp2(m[rb] - M);
         if (a.kv_split <= 0) f *= (L > 0.f ? 1.f / L : 0.f);
-        fsc[rb] = f;
-        float *dst = xb + (((size_t)rg * 2 + (kg ^ 1)) * RB * 16 + srow) * Cf::XSTR + 4 * g;
-        // (constant indices in both branches keep acc in registers)
-        if (kg == 0) {
-#pragma unroll
-            for (int j = 0; j < DH; j++) *reinterpret_cast<f32x4 *>(dst + 16 * j) = acc[rb][DH + j] * f;
-        } else {
-#pragma unroll
-            for (int j = 0; j < DH; j++) *reinterpret_cast<f32x4 *>(dst + 16 * j) = acc[rb][j] * f;
-        }
-        const int rho = lr0 + srow;
-        if (kg == 0 && g == 0 && rho < hnrows) {
-            const int r = seq * p.T + htok0 + rho / GRP, h = kvh * GRP + rho % GRP;
+        const int rho = lrow[rb] + ln;
+        const bool rvalid = rho < hrows[rb];
+        const int r = seq * p.T + htok[rb] + (rvalid ? rho / GRP : 0), h = kvh * GRP + (rvalid ? rho % GRP : 0);
+        if (kg == 0 && g == 0 && rvalid) {
             if (a.kv_split > 0) {
                 const size_t pi = ((size_t)r * NQ + h) * a.part.ns_cap + sp;
                 a.part.m[pi] = M; a.part.l[pi] = L;
@@ -364,22 +563,31 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
                 p.lse[(size_t)r * NQ + h] = (L > 0.f) ? (M + log2f(L)) * kLn2 : kNegInf;
             }
         }
-    }
-    __syncthreads();
-    // Output dims of this wave: blocks [OWN*DH, (OWN+1)*DH) of its accumulator (OWN a constant, so acc stays in
-    // registers).
-    auto finish = [&](auto own_c) {
-        constexpr int OWN = decltype(own_c)::value;
+        // park the blocks of the other owners (constant indices keep acc in registers)
+        static_for<KG>([&](auto o_c) {
+            constexpr int O = decltype(o_c)::value;
+            if (O == kg) return;
+            float *dst = xb + ((((size_t)rg * KG + O) * (KG - 1) + slot(kg, O)) * 16 + ln) * Cf::XSTR + 4 * g;
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++) {
-            const int srow = rb * 16 + ln, rho = lr0 + srow;
-            if (rho >= hnrows) continue;
-            const int r = seq * p.T + htok0 + rho / GRP, h = kvh * GRP + rho % GRP;
-            const float *src = xb + (((size_t)rg * 2 + OWN) * RB * 16 + srow) * Cf::XSTR + 4 * g;
+            for (int j = 0; j < DO; j++) *reinterpret_cast<f32x4 *>(dst + 16 * j) = acc[rb][O * DO + j] * f;
+        });
+        __syncthreads();
+        static_for<KG>([&](auto o_c) {
+            constexpr int O = decltype(o_c)::value;
+            if (O != kg || !rvalid) return;
 #pragma unroll
-            for (int j = 0; j < DH; j++) {
-                const int d = 16 * (OWN * DH + j) + 4 * g;
-                const f32x4 o = acc[rb][OWN * DH + j] * fsc[rb] + *reinterpret_cast<const f32x4 *>(src + 16 * j);
+            for (int j = 0; j < DO; j++) {
+                f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int k = 0; k < KG; k++) {
+                    if (k == O) o = (k == 0) ? acc[rb][O * DO + j] * f : o + acc[rb][O * DO + j] * f;
+                    else {
+                        const f32x4 x = *reinterpret_cast<const f32x4 *>(
+                            xb + ((((size_t)rg * KG + O) * (KG - 1) + slot(k, O)) * 16 + ln) * Cf::XSTR + 4 * g + 16 * j);
+                        o = (k == 0) ? x : o + x;
+                    }
+                }
+                const int d = 16 * (O * DO + j) + 4 * g;
                 if (a.kv_split > 0) {
                     const size_t pi = ((size_t)r * NQ + h) * a.part.ns_cap + sp;
                     *reinterpret_cast<f32x4 *>(a.part.acc + pi * HD + d) = o;
@@ -392,10 +600,9 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
                     *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(p.O) + ob) = wv;
                 }
             }
-        }
-    };
-    if (kg == 0) finish(std::integral_constant<int, 0>{});
-    else finish(std::integral_constant<int, 1>{});
+        });
+        if (rb + 1 < RB) __syncthreads();                               // the next block reuses the exchange
+    }
 }
 
 // ---------------------------------------------------------------- host side
@@ -403,19 +610,25 @@ __global__ void __launch_bounds__(RG * KG_ * 64) prefill_kernel(const PrefArgs a
 // traffic) as 4 row groups x 2 key groups, 16 rows and HD accumulator columns per wave, a 64-row workgroup tile
 // (two 32-row half tiles), 64-key steps (two 16-key sub-tiles per wave) in two LDS stages. HD 512: 4 waves, a
 // 32-row tile, 32-key steps (a 32-key stage of HD 512 is 64 KB).
+// HD 128/256: 4 waves (2 row groups x 2 key groups) over a 32-row tile with 64 KB of LDS (two stages), so two
+// workgroups share a CU: the L2 -> LDS stream of one 8-wave workgroup with a barrier per step was measured at
+// ~42 B/clk per CU, two 4-wave workgroups at ~57-60 B/clk, and the causal prompt is L2-bandwidth-bound at this
+// size (64 query rows per CU). WPE: waves per SIMD the register allocation must allow. PAIR: whether a
+// workgroup may take the causal half-tile pair (i, n-1-i) (one workgroup per CU) instead of neighbours.
 template <int HD> struct PrefTile;
-template <> struct PrefTile<128> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 2; };
-template <> struct PrefTile<256> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 2; };
-template <> struct PrefTile<512> { static constexpr int RB = 1, RG = 2, KG = 2, NS = 2, NSUB = 1; };
+template <> struct PrefTile<128> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 2, WPE = 2; static constexpr bool PAIR = true, MIX = false; };
+template <> struct PrefTile<256> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 2, WPE = 2; static constexpr bool PAIR = true, MIX = false; };
+template <> struct PrefTile<512> { static constexpr int RB = 1, RG = 2, KG = 2, NS = 2, NSUB = 1, WPE = 1; static constexpr bool PAIR = true, MIX = false; };
 template <int HD>
-using PrefTileCfg = PrefCfg<HD, PrefTile<HD>::RB, PrefTile<HD>::RG, PrefTile<HD>::KG, PrefTile<HD>::NS, PrefTile<HD>::NSUB>;
+using PrefTileCfg = PrefCfg<HD, PrefTile<HD>::RB, PrefTile<HD>::RG, PrefTile<HD>::KG, PrefTile<HD>::NS, PrefTile<HD>::NSUB,
+                            PrefTile<HD>::MIX>;
 
 template <int HD, int KVT, int QT, int OT>
 static hipError_t launch_pref_t(const PrefArgs &a, dim3 grid, hipStream_t st) {
     using T = PrefTile<HD>;
     using Cf = PrefTileCfg<HD>;
     static bool configured = false;
-    auto kern = prefill_kernel<HD, T::RB, T::RG, T::KG, T::NS, T::NSUB, KVT, QT, OT>;
+    auto kern = prefill_kernel<HD, T::RB, T::RG, T::KG, T::NS, T::NSUB, T::MIX, T::WPE, KVT, QT, OT>;
     if (!configured) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cf::LDS);
@@ -444,9 +657,15 @@ static int pref_half_rows(int HD) {
     default: return 0;
     }
 }
+// Workgroups of the tile shape resident per CU, and whether it takes causal half-tile pairs.
+static int pref_per_cu(int HD) {
+    const size_t lds = HD == 128 ? PrefTileCfg<128>::LDS : HD == 256 ? PrefTileCfg<256>::LDS : PrefTileCfg<512>::LDS;
+    return (int)std::max<size_t>(1, (160u << 10) / lds);
+}
+static bool pref_pair(int HD) { return HD == 128 ? PrefTile<128>::PAIR : HD == 256 ? PrefTile<256>::PAIR : PrefTile<512>::PAIR; }
 
-// Key split for kv_split = -1: when the unsplit grid would fill at most half of the CUs (a short run of queries
-// over a long cached prefix), cut the keys into as many absolute splits as whole grids fit on the CUs.
+// Key split for kv_split = -1: when the unsplit grid would fill at most half of the workgroup slots (a short run
+// of queries over a long cached prefix), cut the keys into as many absolute splits as whole grids fit on them.
 int prefill_auto_split(const Problem &p) {
     if (p.NQ % p.NKV) return 0;
     const int GRP = p.NQ / p.NKV, HR = pref_half_rows(p.HD);
@@ -456,8 +675,9 @@ int prefill_auto_split(const Problem &p) {
     int dev = 0, ncu = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return 0;
-    if (nwg <= 0 || 2 * nwg > ncu) return 0;
-    const int nsplit = (int)(ncu / nwg);
+    const long slots = (long)ncu * pref_per_cu(p.HD);
+    if (nwg <= 0 || 2 * nwg > slots) return 0;
+    const int nsplit = (int)(slots / nwg);
     const int keys = p.max_pos + 1;
     int ks = (keys + nsplit - 1) / nsplit;
     ks = ((ks + 63) / 64) * 64;
@@ -475,11 +695,15 @@ hipError_t launch_prefill(const Problem &p, int kv_split, const Partials &part, 
     if (kv_split > 0 && nsplit > part.ns_cap) return hipErrorInvalidValue;
     // Pair half tiles (i, n-1-i) when causal work varies across the prompt (no window, prefix shorter than the
     // chunk); otherwise a workgroup takes two neighbouring half tiles.
-    const int pair = (kv_split == 0 && p.window == 0 && nht >= 2 && p.max_pos < 2 * p.T) ? 1 : 0;
+    const int pair = (pref_pair(p.HD) && kv_split == 0 && p.window == 0 && nht >= 2 && p.max_pos < 2 * p.T) ? 1 : 0;
     const int nitems = ((nht + 1) / 2) * nsplit;
     const long nwg = (long)p.nseq * p.NKV * nitems;
     if (nwg <= 0 || nwg > (1L << 30)) return hipErrorInvalidConfiguration;
-    PrefArgs a{p, part, kv_split, nht, nsplit, tqh, pair, nitems, (int)nwg, p.scale * kLog2e};
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        ncu = 0;
+    const int fold = (pref_per_cu(p.HD) >= 2 && nwg <= (long)pref_per_cu(p.HD) * ncu) ? 1 : 0;
+    PrefArgs a{p, part, kv_split, nht, nsplit, tqh, pair, nitems, (int)nwg, p.scale * kLog2e, fold};
     dim3 grid((unsigned)(8 * ((nwg + 7) / 8)));
     hipError_t e = hipErrorInvalidValue;
     const int kv = p.kv_dtype, q = p.q_dtype, o = p.o_dtype;
