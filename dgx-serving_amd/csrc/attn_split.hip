@@ -116,17 +116,25 @@ __device__ __forceinline__ void seg_scan(const Problem &p, int tpb, int nchunks,
     px = __builtin_amdgcn_readfirstlane(px); pq = __builtin_amdgcn_readfirstlane(pq);
 }
 
-// LSE combine of the chunk partials of one (row, head) by one wave. Lane c holds the statistics of chunk c (64
-// at a time); lane d holds 4 head dims. The partial accumulators of the first NB chunks are requested before
-// the statistics are reduced, so a row with up to NB chunks costs one memory round trip. Chunks are summed in
-// increasing order, each weighted by 2^(m_c - max m) (a fixed order: the result depends only on the row).
+// LSE combine of the chunk partials of one (row, head) by one workgroup of 8 * HD / 4 threads: thread (phase ph,
+// 4-dim group d4) sums the chunks c = ph, ph + 8, ... of the row, each weighted by 2^(m_c - max m), in increasing
+// order; the 8 phase sums are then added in phase order. All of a row's partial accumulators up to 64 chunks are
+// requested at once (8 per thread), so such a row costs one memory round trip whatever the head dim. The order
+// depends only on the row's chunk count: a row's result does not depend on the batch.
+constexpr int kCombPh = 8;                           // chunk phases of the combine
+template <int HD> struct CombineCfg {
+    static constexpr int D4 = HD / 4, NT = kCombPh * D4, NW = NT / 64;
+    static constexpr int NB = 8;                     // partial rows in flight per thread (64 chunks per workgroup)
+};
+
 template <int HD>
-__device__ __forceinline__ void combine_wave(const Problem &p, const Partials &part, int C, int s, int t, int h) {
-    constexpr int D4 = HD / 4;                       // 4-dim groups of a row
-    constexpr int NP = (D4 + 63) / 64;               // passes of 64 lanes over the row
-    constexpr int NB = 16;                           // partial rows in flight per lane (the chunks of 8K keys at 512)
-    const int lane = threadIdx.x & 63;
-    const int r = s * p.T + t;
+__global__ void __launch_bounds__(CombineCfg<HD>::NT) combine_kernel(const Problem p, const Partials part, int C) {
+    using Cf = CombineCfg<HD>;
+    constexpr int D4 = Cf::D4, NB = Cf::NB, NW = Cf::NW;
+    __shared__ float red[2 * NW];
+    __shared__ f32x4 sum[kCombPh - 1][D4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, ph = tid / D4, d4 = tid % D4;
+    const int rh = blockIdx.x, r = rh / p.NQ, h = rh % p.NQ, s = r / p.T, t = r % p.T;
     int c_lo, n;
     if (part.seg_g > 0) {                            // verify_kernel's runs: slots 0 .. n-1 of the row's pair
         const int z = s * part.seg_nchunks + t / part.seg_tpb, kvh = h / (p.NQ / p.NKV);
@@ -140,78 +148,89 @@ __device__ __forceinline__ void combine_wave(const Problem &p, const Partials &p
         c_lo = lo / C; n = pos / C - c_lo + 1;
     }
     const size_t base = ((size_t)r * p.NQ + h) * part.ns_cap + c_lo;
-    const float *accb = part.acc + base * HD;
+    const float *accb = part.acc + base * HD + 4 * d4;
+    // Statistics of chunks tid, tid + NT, ... (the first are requested ahead of the accumulators).
+    float m0 = kNegInf, l0 = 0.f;
+    if (tid < n) { m0 = part.m[base + tid]; l0 = part.l[base + tid]; }
     f32x4 v[NB];
-    auto load_batch = [&](int c0, int d4) {
+    float mc[NB];
+    auto load_batch = [&](int c0) {                  // chunks c0 + ph + 8 u
 #pragma unroll
-        for (int u = 0; u < NB; u++) v[u] = *reinterpret_cast<const f32x4 *>(accb + (size_t)min(c0 + u, n - 1) * HD + 4 * d4);
+        for (int u = 0; u < NB; u++) {
+            const int c = c0 + ph + kCombPh * u;
+            mc[u] = kNegInf;
+            if (c < n) {
+                v[u] = *reinterpret_cast<const f32x4 *>(accb + (size_t)c * HD);
+                mc[u] = part.m[base + c];
+            }
+        }
     };
-    load_batch(0, min(lane, D4 - 1));                // in flight while the statistics are reduced
-    const float m0 = lane < n ? part.m[base + lane] : kNegInf;
-    const float l0 = lane < n ? part.l[base + lane] : 0.f;
-    float mg = m0;
-    for (int c0 = 64; c0 < n; c0 += 64)
-        if (c0 + lane < n) mg = fmaxf(mg, part.m[base + c0 + lane]);
-    mg = wave_max(mg);
-    float L = wave_sum((m0 != kNegInf && mg != kNegInf) ? l0 * fast_exp2(m0 - mg) : 0.f);
-    for (int c0 = 64; c0 < n; c0 += 64) {
-        float x = 0.f;
-        if (c0 + lane < n && mg != kNegInf) {
-            const float mc = part.m[base + c0 + lane];
-            if (mc != kNegInf) x = part.l[base + c0 + lane] * fast_exp2(mc - mg);
+    load_batch(0);                                   // in flight while the statistics are reduced
+    // Row statistics: max of m, then L = sum of l_c 2^(m_c - max) (thread-strided, then wave, then wave order).
+    float mx = m0;
+    for (int c = tid + Cf::NT; c < n; c += Cf::NT) mx = fmaxf(mx, part.m[base + c]);
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    float mg = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NW; w++) mg = fmaxf(mg, red[w]);
+    float x = 0.f;
+    if (mg != kNegInf) {
+        if (m0 != kNegInf) x = l0 * fast_exp2(m0 - mg);
+        for (int c = tid + Cf::NT; c < n; c += Cf::NT) {
+            const float m = part.m[base + c];
+            if (m != kNegInf) x += part.l[base + c] * fast_exp2(m - mg);
         }
-        L += wave_sum(x);
     }
+    x = wave_sum(x);
+    if (lane == 0) red[NW + wave] = x;
+    __syncthreads();
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) L += red[NW + w];
+    // This thread's phase sum.
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < n; c0 += kCombPh * NB) {
+        if (c0 > 0) load_batch(c0);
+#pragma unroll
+        for (int u = 0; u < NB; u++) {
+            if (mc[u] != kNegInf && mg != kNegInf) acc += v[u] * fast_exp2(mc[u] - mg);
+        }
+    }
+    if (ph > 0) sum[ph - 1][d4] = acc;
+    __syncthreads();
+    if (ph > 0) return;
+#pragma unroll
+    for (int k = 0; k < kCombPh - 1; k++) acc += sum[k][d4];
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    const float w0 = (m0 != kNegInf && mg != kNegInf) ? fast_exp2(m0 - mg) : 0.f;
+    f32x4 o = acc * inv;
+    const size_t oi = ((size_t)r * p.NQ + h) * HD + 4 * d4;
+    if (p.gate) {                                    // output gate: o *= 1 / (1 + 2^(-g log2 e))
+        float gv[4];
+        if (p.gate_dtype == DT_FP32) {
+            const f32x4 gg = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(p.gate) + oi);
+            gv[0] = gg.x; gv[1] = gg.y; gv[2] = gg.z; gv[3] = gg.w;
+        } else {
+            const u32x2 gw = *reinterpret_cast<const u32x2 *>(reinterpret_cast<const uint16_t *>(p.gate) + oi);
+            const bool f16 = p.gate_dtype == DT_F16;
 #pragma unroll
-    for (int ps = 0; ps < NP; ps++) {
-        const int d4 = lane + 64 * ps;
-        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int c0 = 0; c0 < n; c0 += NB) {
-            if (ps > 0 || c0 > 0) load_batch(c0, min(d4, D4 - 1));
-            float w = w0;                            // weights of the 64-chunk group holding this batch
-            if (c0 >= 64) {
-                const int c = (c0 & ~63) + lane;
-                const float mc = c < n ? part.m[base + c] : kNegInf;
-                w = (mc != kNegInf && mg != kNegInf) ? fast_exp2(mc - mg) : 0.f;
-            }
-#pragma unroll
-            for (int u = 0; u < NB; u++) {
-                const float wc = __shfl(w, (c0 + u) & 63);
-                if (c0 + u < n && wc != 0.f) acc += v[u] * wc;
+            for (int e = 0; e < 4; e++) {
+                const uint16_t b16 = (uint16_t)(gw[e / 2] >> (16 * (e & 1)));
+                gv[e] = f16 ? f16_bits_to_f32(b16) : bf16_bits_to_f32(b16);
             }
         }
-        if (d4 < D4) {
-            f32x4 o = acc * inv;
-            const size_t oi = ((size_t)r * p.NQ + h) * HD + 4 * d4;
-            if (p.gate) {                                // output gate: o *= 1 / (1 + 2^(-g log2 e))
-                float gv[4];
-                if (p.gate_dtype == DT_FP32) {
-                    const f32x4 gg = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(p.gate) + oi);
-                    gv[0] = gg.x; gv[1] = gg.y; gv[2] = gg.z; gv[3] = gg.w;
-                } else {
-                    const u32x2 gw = *reinterpret_cast<const u32x2 *>(reinterpret_cast<const uint16_t *>(p.gate) + oi);
-                    const bool f16 = p.gate_dtype == DT_F16;
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const uint16_t b16 = (uint16_t)(gw[e / 2] >> (16 * (e & 1)));
-                        gv[e] = f16 ? f16_bits_to_f32(b16) : bf16_bits_to_f32(b16);
-                    }
-                }
-#pragma unroll
-                for (int e = 0; e < 4; e++) o[e] *= 1.f / (1.f + fast_exp2(-gv[e] * kLog2e));
-            }
-            if (p.o_dtype == DT_FP32) *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.O) + oi) = o;
-            else {
-                const bool f16 = p.o_dtype == DT_F16;
-                const u32x2 ow = u32x2{(uint32_t)f32_to_op(o.x, f16) | ((uint32_t)f32_to_op(o.y, f16) << 16),
-                                       (uint32_t)f32_to_op(o.z, f16) | ((uint32_t)f32_to_op(o.w, f16) << 16)};
-                *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(p.O) + oi) = ow;
-            }
-        }
+        for (int e = 0; e < 4; e++) o[e] *= 1.f / (1.f + fast_exp2(-gv[e] * kLog2e));
     }
-    if (p.lse && lane == 0) p.lse[(size_t)r * p.NQ + h] = (L > 0.f) ? (mg + log2f(L)) * kLn2 : kNegInf;
+    if (p.o_dtype == DT_FP32) *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.O) + oi) = o;
+    else {
+        const bool f16 = p.o_dtype == DT_F16;
+        const u32x2 ow = u32x2{(uint32_t)f32_to_op(o.x, f16) | ((uint32_t)f32_to_op(o.y, f16) << 16),
+                               (uint32_t)f32_to_op(o.z, f16) | ((uint32_t)f32_to_op(o.w, f16) << 16)};
+        *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(p.O) + oi) = ow;
+    }
+    if (p.lse && tid == 0) p.lse[(size_t)r * p.NQ + h] = (L > 0.f) ? (mg + log2f(L)) * kLn2 : kNegInf;
 }
 
 template <int HD, int RB>
@@ -226,7 +245,7 @@ struct SplitCfg {
     static constexpr int CPT = KT * HD / 8 / (NW * 64);   // 16-byte chunks per thread per tile (K and V each)
     static constexpr int NSTG = 2;                          // register stages of the K/V stream
     static constexpr size_t TILE = (size_t)KT * STR;      // elements of one K or V tile
-    static constexpr bool QREG = RB * KS <= 8;            // Q fragments live in registers (straight from HBM)
+    static constexpr bool QREG = RB * KS <= 16;           // Q fragments live in registers (straight from HBM)
     static constexpr size_t LDS = ((QREG ? 0 : (size_t)RR * STR) + 4 * TILE) * 2;   // [Q] + (K, V) x double buffer
     static_assert(CPT >= 1 && (KT * HD / 8) % (NW * 64) == 0, "tile chunks");
 };
@@ -675,15 +694,6 @@ __global__ void __launch_bounds__(256) verify_kernel(const SplitArgs a) {
     }
 }
 
-// LSE combine: one wave per (row, head).
-constexpr int kCombineWaves = 2;       // two waves per workgroup: the (row, head) waves spread over more CUs
-template <int HD>
-__global__ void __launch_bounds__(kCombineWaves * 64) combine_kernel(const Problem p, const Partials part, int C) {
-    const int rh = blockIdx.x * kCombineWaves + (threadIdx.x >> 6);
-    if (rh >= p.nseq * p.T * p.NQ) return;
-    const int r = rh / p.NQ, h = rh % p.NQ;
-    combine_wave<HD>(p, part, C, r / p.T, r % p.T, h);
-}
 
 // ---------------------------------------------------------------- host side
 // verify_kernel's grid: the workgroups that are resident at once on the current device (per device, cached).
@@ -812,11 +822,12 @@ hipError_t launch_split(const Problem &p, int chunk, Partials &part, hipStream_t
 
 hipError_t launch_combine(const Problem &p, int chunk, const Partials &part, hipStream_t st) {
     const int rows = p.nseq * p.T * p.NQ;
-    dim3 grid((rows + kCombineWaves - 1) / kCombineWaves), blk(kCombineWaves * 64);
+    if (rows <= 0) return hipSuccess;
+    const dim3 grid((unsigned)rows);
     switch (p.HD) {
-    case 128: hipLaunchKernelGGL(combine_kernel<128>, grid, blk, 0, st, p, part, chunk); break;
-    case 256: hipLaunchKernelGGL(combine_kernel<256>, grid, blk, 0, st, p, part, chunk); break;
-    case 512: hipLaunchKernelGGL(combine_kernel<512>, grid, blk, 0, st, p, part, chunk); break;
+    case 128: hipLaunchKernelGGL(combine_kernel<128>, grid, dim3(CombineCfg<128>::NT), 0, st, p, part, chunk); break;
+    case 256: hipLaunchKernelGGL(combine_kernel<256>, grid, dim3(CombineCfg<256>::NT), 0, st, p, part, chunk); break;
+    case 512: hipLaunchKernelGGL(combine_kernel<512>, grid, dim3(CombineCfg<512>::NT), 0, st, p, part, chunk); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
