@@ -116,25 +116,32 @@ __device__ __forceinline__ void seg_scan(const Problem &p, int tpb, int nchunks,
     px = __builtin_amdgcn_readfirstlane(px); pq = __builtin_amdgcn_readfirstlane(pq);
 }
 
-// LSE combine of the chunk partials of one (row, head) by one workgroup of 8 * HD / 4 threads: thread (phase ph,
-// 4-dim group d4) sums the chunks c = ph, ph + 8, ... of the row, each weighted by 2^(m_c - max m), in increasing
-// order; the 8 phase sums are then added in phase order. All of a row's partial accumulators up to 64 chunks are
-// requested at once (8 per thread), so such a row costs one memory round trip whatever the head dim. The order
-// depends only on the row's chunk count: a row's result does not depend on the batch.
-constexpr int kCombPh = 8;                           // chunk phases of the combine
+// LSE combine of the chunk partials of one (row, head) by a row group of PH * HD / 4 threads: thread (phase ph,
+// 4-dim group d4) sums the chunks c = ph, ph + PH, ... of the row, each weighted by 2^(m_c - max m), in increasing
+// order; the PH phase sums are then added in phase order. NB chunks per thread are requested at once, so a row of
+// up to PH * NB chunks costs one memory round trip. HD 512 rows (a 32K-key cache holds 64 chunks of 512 keys, at
+// 2 KB of partial each) take eight phases; narrower rows take one wave each. The phase count depends
+// only on the head dim: a row's result does not depend on the batch.
 template <int HD> struct CombineCfg {
-    static constexpr int D4 = HD / 4, NT = kCombPh * D4, NW = NT / 64;
-    static constexpr int NB = 8;                     // partial rows in flight per thread (64 chunks per workgroup)
+    static constexpr int PH = HD >= 512 ? 8 : 256 / HD;   // chunk phases per row (a row is at least one wave)
+    static constexpr int D4 = HD / 4, RT = PH * D4;  // threads per row
+    static constexpr int NR = RT >= 128 ? 1 : 128 / RT;   // rows per workgroup
+    static constexpr int NT = NR * RT, NWR = (RT + 63) / 64;   // threads, waves per row
+    static constexpr int NB = PH >= 8 ? 8 : 16;      // partial rows in flight per thread
+    static_assert(RT % 64 == 0, "a row is whole waves");
 };
 
 template <int HD>
 __global__ void __launch_bounds__(CombineCfg<HD>::NT) combine_kernel(const Problem p, const Partials part, int C) {
     using Cf = CombineCfg<HD>;
-    constexpr int D4 = Cf::D4, NB = Cf::NB, NW = Cf::NW;
-    __shared__ float red[2 * NW];
-    __shared__ f32x4 sum[kCombPh - 1][D4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, ph = tid / D4, d4 = tid % D4;
-    const int rh = blockIdx.x, r = rh / p.NQ, h = rh % p.NQ, s = r / p.T, t = r % p.T;
+    constexpr int D4 = Cf::D4, NB = Cf::NB, NWR = Cf::NWR, PH = Cf::PH, NR = Cf::NR;
+    __shared__ float red[NR][2 * NWR];
+    __shared__ f32x4 sum[NR][PH > 1 ? PH - 1 : 1][D4];
+    const int tid = threadIdx.x, lane = tid & 63, rg = tid / Cf::RT, rt = tid % Cf::RT;
+    const int wave = rt >> 6, ph = rt / D4, d4 = rt % D4;
+    const int rh = blockIdx.x * NR + rg;
+    const bool live = rh < p.nseq * p.T * p.NQ;      // row-group uniform (whole waves)
+    const int rr = live ? rh : 0, r = rr / p.NQ, h = rr % p.NQ, s = r / p.T, t = r % p.T;
     int c_lo, n;
     if (part.seg_g > 0) {                            // verify_kernel's runs: slots 0 .. n-1 of the row's pair
         const int z = s * part.seg_nchunks + t / part.seg_tpb, kvh = h / (p.NQ / p.NKV);
@@ -147,17 +154,18 @@ __global__ void __launch_bounds__(CombineCfg<HD>::NT) combine_kernel(const Probl
         const int pos = tok_pos(p, s, t), lo = win_lo(pos, p.window);
         c_lo = lo / C; n = pos / C - c_lo + 1;
     }
+    if (!live) n = 0;
     const size_t base = ((size_t)r * p.NQ + h) * part.ns_cap + c_lo;
     const float *accb = part.acc + base * HD + 4 * d4;
-    // Statistics of chunks tid, tid + NT, ... (the first are requested ahead of the accumulators).
+    // Statistics of chunks rt, rt + RT, ... (the first are requested ahead of the accumulators).
     float m0 = kNegInf, l0 = 0.f;
-    if (tid < n) { m0 = part.m[base + tid]; l0 = part.l[base + tid]; }
+    if (rt < n) { m0 = part.m[base + rt]; l0 = part.l[base + rt]; }
     f32x4 v[NB];
     float mc[NB];
-    auto load_batch = [&](int c0) {                  // chunks c0 + ph + 8 u
+    auto load_batch = [&](int c0) {                  // chunks c0 + ph + PH u
 #pragma unroll
         for (int u = 0; u < NB; u++) {
-            const int c = c0 + ph + kCombPh * u;
+            const int c = c0 + ph + PH * u;
             mc[u] = kNegInf;
             if (c < n) {
                 v[u] = *reinterpret_cast<const f32x4 *>(accb + (size_t)c * HD);
@@ -168,41 +176,49 @@ __global__ void __launch_bounds__(CombineCfg<HD>::NT) combine_kernel(const Probl
     load_batch(0);                                   // in flight while the statistics are reduced
     // Row statistics: max of m, then L = sum of l_c 2^(m_c - max) (thread-strided, then wave, then wave order).
     float mx = m0;
-    for (int c = tid + Cf::NT; c < n; c += Cf::NT) mx = fmaxf(mx, part.m[base + c]);
+    for (int c = rt + Cf::RT; c < n; c += Cf::RT) mx = fmaxf(mx, part.m[base + c]);
     mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    float mg = kNegInf;
+    float mg = mx;
+    if constexpr (NWR > 1) {
+        if (lane == 0) red[rg][wave] = mx;
+        __syncthreads();
+        mg = kNegInf;
 #pragma unroll
-    for (int w = 0; w < NW; w++) mg = fmaxf(mg, red[w]);
+        for (int w = 0; w < NWR; w++) mg = fmaxf(mg, red[rg][w]);
+    }
     float x = 0.f;
     if (mg != kNegInf) {
         if (m0 != kNegInf) x = l0 * fast_exp2(m0 - mg);
-        for (int c = tid + Cf::NT; c < n; c += Cf::NT) {
+        for (int c = rt + Cf::RT; c < n; c += Cf::RT) {
             const float m = part.m[base + c];
             if (m != kNegInf) x += part.l[base + c] * fast_exp2(m - mg);
         }
     }
-    x = wave_sum(x);
-    if (lane == 0) red[NW + wave] = x;
-    __syncthreads();
-    float L = 0.f;
+    float L = wave_sum(x);
+    if constexpr (NWR > 1) {
+        if (lane == 0) red[rg][NWR + wave] = L;
+        __syncthreads();
+        L = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; w++) L += red[NW + w];
+        for (int w = 0; w < NWR; w++) L += red[rg][NWR + w];
+    }
     // This thread's phase sum.
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int c0 = 0; c0 < n; c0 += kCombPh * NB) {
+    for (int c0 = 0; c0 < n; c0 += PH * NB) {
         if (c0 > 0) load_batch(c0);
 #pragma unroll
         for (int u = 0; u < NB; u++) {
             if (mc[u] != kNegInf && mg != kNegInf) acc += v[u] * fast_exp2(mc[u] - mg);
         }
     }
-    if (ph > 0) sum[ph - 1][d4] = acc;
-    __syncthreads();
-    if (ph > 0) return;
+    if constexpr (PH > 1) {
+        if (ph > 0) sum[rg][ph - 1][d4] = acc;
+        __syncthreads();
+        if (ph > 0) return;
 #pragma unroll
-    for (int k = 0; k < kCombPh - 1; k++) acc += sum[k][d4];
+        for (int k = 0; k < PH - 1; k++) acc += sum[rg][k][d4];
+    }
+    if (!live) return;
     const float inv = L > 0.f ? 1.f / L : 0.f;
     f32x4 o = acc * inv;
     const size_t oi = ((size_t)r * p.NQ + h) * HD + 4 * d4;
@@ -230,7 +246,7 @@ __global__ void __launch_bounds__(CombineCfg<HD>::NT) combine_kernel(const Probl
                                (uint32_t)f32_to_op(o.z, f16) | ((uint32_t)f32_to_op(o.w, f16) << 16)};
         *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(p.O) + oi) = ow;
     }
-    if (p.lse && tid == 0) p.lse[(size_t)r * p.NQ + h] = (L > 0.f) ? (mg + log2f(L)) * kLn2 : kNegInf;
+    if (p.lse && rt == 0) p.lse[(size_t)r * p.NQ + h] = (L > 0.f) ? (mg + log2f(L)) * kLn2 : kNegInf;
 }
 
 template <int HD, int RB>
@@ -823,11 +839,11 @@ hipError_t launch_split(const Problem &p, int chunk, Partials &part, hipStream_t
 hipError_t launch_combine(const Problem &p, int chunk, const Partials &part, hipStream_t st) {
     const int rows = p.nseq * p.T * p.NQ;
     if (rows <= 0) return hipSuccess;
-    const dim3 grid((unsigned)rows);
+    auto grid = [&](int nr) { return dim3((unsigned)((rows + nr - 1) / nr)); };
     switch (p.HD) {
-    case 128: hipLaunchKernelGGL(combine_kernel<128>, grid, dim3(CombineCfg<128>::NT), 0, st, p, part, chunk); break;
-    case 256: hipLaunchKernelGGL(combine_kernel<256>, grid, dim3(CombineCfg<256>::NT), 0, st, p, part, chunk); break;
-    case 512: hipLaunchKernelGGL(combine_kernel<512>, grid, dim3(CombineCfg<512>::NT), 0, st, p, part, chunk); break;
+    case 128: hipLaunchKernelGGL(combine_kernel<128>, grid(CombineCfg<128>::NR), dim3(CombineCfg<128>::NT), 0, st, p, part, chunk); break;
+    case 256: hipLaunchKernelGGL(combine_kernel<256>, grid(CombineCfg<256>::NR), dim3(CombineCfg<256>::NT), 0, st, p, part, chunk); break;
+    case 512: hipLaunchKernelGGL(combine_kernel<512>, grid(CombineCfg<512>::NR), dim3(CombineCfg<512>::NT), 0, st, p, part, chunk); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
