@@ -49,9 +49,9 @@ __device__ __forceinline__ const KE *kv_base(const Problem &p, bool v, int s) {
 struct Partials {
     float *m, *l, *acc;
     int ns_cap;
-    // Set by launch_split when verify_kernel wrote the partials (seg_g > 0: its grid size, minimum run length and
-    // token tiling); 0 for partials indexed by absolute key chunk.
-    int seg_g = 0, seg_qmin = 0, seg_tpb = 0, seg_nchunks = 0;
+    // Set by launch_split when verify_kernel wrote the partials (seg_g > 0: its grid size and minimum run length;
+    // the slots of a pair end at the first slot whose m is +inf); 0 for partials indexed by absolute key chunk.
+    int seg_g = 0, seg_qmin = 0;
 };
 
 // Position of token t of sequence s, and the first key of its sliding window.

@@ -58,7 +58,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 // are cut into equal runs of q tiles, one run per workgroup of a grid of resident workgroups, so every workgroup
 // streams the same number of bytes whatever the mix of sequence lengths (a grid of fixed key chunks leaves a
 // partly filled last round of workgroups). A run writes one partial per pair it meets, into slot (workgroup index
-// - index of the pair's first workgroup); the combine derives the same slots from the positions. q depends on the
+// - index of the pair's first workgroup); the last run of a pair marks the slot after its own for the combine. q depends on the
 // total tile count, so verify results depend on the batch; they are deterministic for given inputs.
 struct SegPair { int seq, tok0, tok1, lo, hi, jb, n; };
 
@@ -142,19 +142,23 @@ __global__ void __launch_bounds__(CombineCfg<HD>::NT) combine_kernel(const Probl
     const int rh = blockIdx.x * NR + rg;
     const bool live = rh < p.nseq * p.T * p.NQ;      // row-group uniform (whole waves)
     const int rr = live ? rh : 0, r = rr / p.NQ, h = rr % p.NQ, s = r / p.T, t = r % p.T;
-    int c_lo, n;
-    if (part.seg_g > 0) {                            // verify_kernel's runs: slots 0 .. n-1 of the row's pair
-        const int z = s * part.seg_nchunks + t / part.seg_tpb, kvh = h / (p.NQ / p.NKV);
-        int N, zx, px, pz;
-        seg_scan(p, part.seg_tpb, part.seg_nchunks, INT_MAX, z, N, zx, px, pz);
-        const int q = max((N + part.seg_g - 1) / part.seg_g, part.seg_qmin);
-        const int nz = seg_pair_u(p, part.seg_tpb, part.seg_nchunks, z).n, S = pz + kvh * nz;
-        c_lo = 0; n = min((S + nz - 1) / q - S / q + 1, part.ns_cap);
-    } else {
+    // Chunks [c_lo, c_lo + n) of the row. verify_kernel's partials sit in slots 0 .. n-1, and its last run of each
+    // pair marks slot n (when there is one) with m = +inf: n is the first marked slot (every wave finds the same).
+    int c_lo = 0, n = 0;
+    if (!live) {
+    } else if (part.seg_g == 0) {
         const int pos = tok_pos(p, s, t), lo = win_lo(pos, p.window);
         c_lo = lo / C; n = pos / C - c_lo + 1;
+    } else {
+        const size_t b0 = ((size_t)r * p.NQ + h) * part.ns_cap;
+        n = part.ns_cap;
+        for (int c0 = 0; c0 < part.ns_cap; c0 += 64) {
+            const int c = c0 + lane;
+            const float mv = c < part.ns_cap ? part.m[b0 + c] : kPosInf;
+            const unsigned long long hit = __ballot(mv == kPosInf);
+            if (hit) { n = c0 + __builtin_ctzll(hit); break; }
+        }
     }
-    if (!live) n = 0;
     const size_t base = ((size_t)r * p.NQ + h) * part.ns_cap + c_lo;
     const float *accb = part.acc + base * HD + 4 * d4;
     // Statistics of chunks rt, rt + RT, ... (the first are requested ahead of the accumulators).
@@ -543,11 +547,12 @@ struct VerifyCfg {
     static_assert(NLD >= 1 && (KT * SLOTS) % (NW * 64) == 0, "tile loads");
 };
 
-// Tiles [t0, t1) of pair sp, KV head kvh (keys sp.jb + 16 t ..), into partial slot `slot`. Called by all waves;
+// Tiles [t0, t1) of pair sp, KV head kvh (keys sp.jb + 16 t ..), into partial slot `slot`; `last`: the run ends
+// the pair, and marks the next slot (if any) as the end of the pair's slots for the combine. Called by all waves;
 // returns with every load landed (the caller's barrier then frees the ring).
 template <int HD, int RB, int KVT, int QT>
 __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair &sp, int kvh, int t0, int t1, int slot,
-                                               unsigned char *smem) {
+                                               bool last, unsigned char *smem) {
     using Cf = VerifyCfg<HD>;
     constexpr int NS = Cf::NS, KT = Cf::KT, KS = Cf::KS, DB = Cf::DB, NLD = Cf::NLD, SLOTS = Cf::SLOTS;
     constexpr int ROWB = Cf::ROWB;
@@ -588,10 +593,11 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
     if (p.anc) pos_min = min(pos_min, tok_pos(p, seq, 0) - 1);
 
     // Tile k (keys jb + KT k ..) -> stage k % NS. Thread slot S of a tensor's tile holds the 16-byte column
-    // (S % SLOTS) ^ vswz(key) of key row S / SLOTS; keys past the end re-read the last key (they are masked)
-    // and tiles past the segment's last re-read that tile (an L2 hit, not the next run's keys).
+    // (S % SLOTS) ^ vswz(key) of key row S / SLOTS; keys past the end re-read the last key (they are masked).
+    // Nothing is issued past the segment's last tile (the loads are non-temporal: a re-read would go to HBM).
     auto issue = [&](int k) {
-        const int jt = jb + KT * min(k, ntile - 1), jrow = key_row(p, jt);
+        if (k >= ntile) return;
+        const int jt = jb + KT * k, jrow = key_row(p, jt);
         unsigned char *kd = smem + (size_t)(k % NS) * Cf::STAGE, *vd = kd + Cf::TILE;
 #pragma unroll
         for (int u = 0; u < NLD; u++) {
@@ -601,7 +607,6 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
             __builtin_amdgcn_global_load_lds((vglb_void *)(Vb + off), (vlds_void *)(vd + (size_t)i * 1024), 16, 0, 2);
         }
     };
-    // Tiles past the last are issued too (stages never read), so every wait sees the same count.
 #pragma unroll
     for (int k = 0; k < NS - 1; k++) issue(k);
 
@@ -615,9 +620,12 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
     const unsigned vaddr = lds0 + Cf::TILE + vr * ROWB + 8 * (ln & 1) + ((((ln & 3) >> 1) ^ vswz(vr)) << 4);
 
     for (int it = 0; it < ntile; it++) {
-        // Tile it landed (NS - 2 younger tiles may still fly); the barrier makes every wave's loads visible and
-        // frees the stage of tile it-1 for tile it+NS-1.
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD * (NS - 2)) : "memory");
+        // Tile it landed (the min(NS - 2, ntile - 1 - it) younger tiles may still fly); the barrier makes every
+        // wave's loads visible and frees the stage of tile it-1 for tile it+NS-1.
+        static_assert(NS == 4, "tail waits");
+        if (it + NS - 2 < ntile) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD * (NS - 2)) : "memory");
+        else if (it + 1 < ntile) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         issue(it + NS - 1);
         // waves past the last row block compute too (their rows are masked): a branch here costs registers
@@ -678,7 +686,10 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
     const size_t pi = ((size_t)r * p.NQ + h) * a.part.ns_cap + slot;
 #pragma unroll
     for (int db = 0; db < DB; db++) *reinterpret_cast<f32x4 *>(a.part.acc + pi * HD + 16 * db + 4 * g) = acc[db];
-    if (g == 0) { a.part.m[pi] = m; a.part.l[pi] = l; }
+    if (g == 0) {
+        a.part.m[pi] = m; a.part.l[pi] = l;
+        if (last && slot + 1 < a.part.ns_cap) a.part.m[pi + 1] = kPosInf;   // end of the pair's slots
+    }
 }
 
 template <int HD, int RB, int KVT, int QT>
@@ -699,7 +710,7 @@ __global__ void __launch_bounds__(256) verify_kernel(const SplitArgs a) {
         const int local = x - P, kvh = local / sp.n, t0 = local % sp.n;
         const int t1 = min(sp.n, t0 + (x1 - x)), slot = w - (P + kvh * sp.n) / q;
         if (kvh >= p.NKV || slot < 0 || slot >= a.part.ns_cap) break;   // unreachable while the counts agree
-        verify_segment<HD, RB, KVT, QT>(a, sp, kvh, t0, t1, slot, smem);
+        verify_segment<HD, RB, KVT, QT>(a, sp, kvh, t0, t1, slot, t1 == sp.n, smem);
         x += t1 - t0;
         if (x >= x1) break;
         if (t1 == sp.n && kvh == p.NKV - 1) {            // next pair (every pair holds at least one tile)
@@ -750,12 +761,10 @@ static hipError_t launch_split_t(SplitArgs &a, dim3 grid, hipStream_t st) {
             hipError_t e = verify_grid<HD, RB, KVT, QT>(G);
             if (e != hipSuccess) return e;
             // q >= qmin keeps a pair within ns_cap slots: a pair of n <= max_pos/16 + 1 tiles meets at most
-            // floor((n - 1) / q) + 2 runs.
+            // floor((n - 1) / q) + 2 runs (with fewer than ns_cap, the slot after the last holds the end mark).
             const int nmax = a.p.max_pos / 16 + 1;
             a.part.seg_g = G;
             a.part.seg_qmin = std::max(8, (nmax - 1) / (a.part.ns_cap - 1) + 1);
-            a.part.seg_tpb = a.tpb;
-            a.part.seg_nchunks = a.nchunks;
             hipLaunchKernelGGL((verify_kernel<HD, RB, KVT, QT>), dim3(G), dim3(256), VerifyCfg<HD>::LDS, st, a);
             return hipGetLastError();
         }
