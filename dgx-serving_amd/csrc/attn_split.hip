@@ -609,6 +609,22 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
     };
 #pragma unroll
     for (int k = 0; k < NS - 1; k++) issue(k);
+    // Tile it landed (the min(NS - 2, ntile - 1 - it) younger tiles may still fly).
+    static_assert(NS == 4, "tail waits");
+    auto wait_tile = [&](int it) {
+        if (it + NS - 2 < ntile) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD * (NS - 2)) : "memory");
+        else if (it + 1 < ntile) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
+    if (!active) {                // a wave past the last row block only streams its share of the ring
+        for (int it = 0; it < ntile; it++) {
+            wait_tile(it);
+            __syncthreads();
+            issue(it + NS - 1);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        return;
+    }
 
     float m = kNegInf, l = 0.f;
     f32x4 acc[DB];
@@ -620,15 +636,10 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
     const unsigned vaddr = lds0 + Cf::TILE + vr * ROWB + 8 * (ln & 1) + ((((ln & 3) >> 1) ^ vswz(vr)) << 4);
 
     for (int it = 0; it < ntile; it++) {
-        // Tile it landed (the min(NS - 2, ntile - 1 - it) younger tiles may still fly); the barrier makes every
-        // wave's loads visible and frees the stage of tile it-1 for tile it+NS-1.
-        static_assert(NS == 4, "tail waits");
-        if (it + NS - 2 < ntile) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD * (NS - 2)) : "memory");
-        else if (it + 1 < ntile) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD) : "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // The barrier makes every wave's loads of tile it visible and frees the stage of tile it-1 for tile it+NS-1.
+        wait_tile(it);
         __syncthreads();
         issue(it + NS - 1);
-        // waves past the last row block compute too (their rows are masked): a branch here costs registers
         const int jt = jb + KT * it;
         const unsigned stage = (it % NS) * Cf::STAGE;
         unsigned kb = kaddr + stage, vb = vaddr + stage;
