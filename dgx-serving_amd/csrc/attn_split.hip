@@ -530,8 +530,12 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
 // ---------------------------------------------------------------- verify / tree kernel (16-bit caches, 2-4 row blocks)
 // The rows-split layout of split_kernel with a deeper K/V stream: tiles go from HBM straight into an NS-stage LDS
 // ring with gfx950 direct-to-LDS loads (no staging registers, so more tiles in flight per workgroup at the same
-// occupancy), rows unpadded with their 16-byte slots XOR-swizzled by the key (swz below). Wave w owns row block w
-// (all head dims); the wave past the last row block only loads.
+// occupancy), rows unpadded with their 16-byte slots XOR-swizzled by the key. Wave w owns row block w (all head
+// dims); the wave past the last row block only loads.
+// Swizzles (slot s of key row k holds head-dim column s ^ swz(k)): K rows are read 16 bytes per lane by key
+// (lane = key ln, column 4 ks + g), so kswz(ln) = ln puts the 8 (16) keys of a lane group on distinct bank quads;
+// V rows are read by the transpose read with lane bit 1 selecting the column, so vswz keeps bit 0 free for it.
+__device__ __forceinline__ int kswz(int k) { return k & 15; }
 __device__ __forceinline__ int vswz(int k) { return ((k & 7) << 1) | ((k >> 3) & 1); }
 typedef __attribute__((address_space(3))) void vlds_void;
 typedef __attribute__((address_space(1))) void vglb_void;
@@ -593,7 +597,7 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
     if (p.anc) pos_min = min(pos_min, tok_pos(p, seq, 0) - 1);
 
     // Tile k (keys jb + KT k ..) -> stage k % NS. Thread slot S of a tensor's tile holds the 16-byte column
-    // (S % SLOTS) ^ vswz(key) of key row S / SLOTS; keys past the end re-read the last key (they are masked).
+    // (S % SLOTS) ^ swz(key) of key row S / SLOTS; keys past the end re-read the last key (they are masked).
     // Nothing is issued past the segment's last tile (the loads are non-temporal: a re-read would go to HBM).
     auto issue = [&](int k) {
         if (k >= ntile) return;
@@ -602,9 +606,10 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
 #pragma unroll
         for (int u = 0; u < NLD; u++) {
             const int i = wave * NLD + u, S = i * 64 + lane, key = S / SLOTS;
-            const size_t off = (size_t)(jrow + min(key, hi_b - 1 - jt)) * krow + (size_t)(((S % SLOTS) ^ vswz(key)) * 8);
-            __builtin_amdgcn_global_load_lds((vglb_void *)(Kb + off), (vlds_void *)(kd + (size_t)i * 1024), 16, 0, 2);
-            __builtin_amdgcn_global_load_lds((vglb_void *)(Vb + off), (vlds_void *)(vd + (size_t)i * 1024), 16, 0, 2);
+            const size_t row = (size_t)(jrow + min(key, hi_b - 1 - jt)) * krow;
+            const size_t ko = row + (size_t)(((S % SLOTS) ^ kswz(key)) * 8), vo = row + (size_t)(((S % SLOTS) ^ vswz(key)) * 8);
+            __builtin_amdgcn_global_load_lds((vglb_void *)(Kb + ko), (vlds_void *)(kd + (size_t)i * 1024), 16, 0, 2);
+            __builtin_amdgcn_global_load_lds((vglb_void *)(Vb + vo), (vlds_void *)(vd + (size_t)i * 1024), 16, 0, 2);
         }
     };
 #pragma unroll
@@ -632,7 +637,7 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
     for (int db = 0; db < DB; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     const unsigned lds0 = (unsigned)(uintptr_t)smem;
     const int vr = 4 * g + (ln >> 2);
-    const unsigned kaddr = lds0 + ln * ROWB + ((g ^ vswz(ln)) << 4);
+    const unsigned kaddr = lds0 + ln * ROWB + ((g ^ kswz(ln)) << 4);
     const unsigned vaddr = lds0 + Cf::TILE + vr * ROWB + 8 * (ln & 1) + ((((ln & 3) >> 1) ^ vswz(vr)) << 4);
 
     for (int it = 0; it < ntile; it++) {
