@@ -597,28 +597,44 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
     if (p.anc) pos_min = min(pos_min, tok_pos(p, seq, 0) - 1);
 
     // Tile k (keys jb + KT k ..) -> stage k % NS. Thread slot S of a tensor's tile holds the 16-byte column
-    // (S % SLOTS) ^ swz(key) of key row S / SLOTS; keys past the end re-read the last key (they are masked).
-    // Nothing is issued past the segment's last tile (the loads are non-temporal: a re-read would go to HBM).
+    // (S % SLOTS) ^ swz(key) of key row S / SLOTS (per-thread offsets below; the tile's first row is a scalar);
+    // keys past the end re-read the last key (they are masked). Nothing is issued past the segment's last tile
+    // (the loads are non-temporal: a re-read would go to HBM).
+    unsigned koff[NLD], voff[NLD];
+#pragma unroll
+    for (int u = 0; u < NLD; u++) {
+        const int S = (wave * NLD + u) * 64 + lane, key = S / SLOTS;
+        koff[u] = (unsigned)(key * krow) + (unsigned)(((S % SLOTS) ^ kswz(key)) * 8);
+        voff[u] = (unsigned)(key * krow) + (unsigned)(((S % SLOTS) ^ vswz(key)) * 8);
+    }
     auto issue = [&](int k) {
         if (k >= ntile) return;
-        const int jt = jb + KT * k, jrow = key_row(p, jt);
+        const int jt = jb + KT * k;
+        const KE *kt = Kb + (size_t)key_row(p, jt) * krow, *vt = Vb + (size_t)key_row(p, jt) * krow;
         unsigned char *kd = smem + (size_t)(k % NS) * Cf::STAGE, *vd = kd + Cf::TILE;
+        const bool whole = jt + KT <= hi_b;              // wave-uniform: only a pair's last tile clamps
 #pragma unroll
         for (int u = 0; u < NLD; u++) {
-            const int i = wave * NLD + u, S = i * 64 + lane, key = S / SLOTS;
-            const size_t row = (size_t)(jrow + min(key, hi_b - 1 - jt)) * krow;
-            const size_t ko = row + (size_t)(((S % SLOTS) ^ kswz(key)) * 8), vo = row + (size_t)(((S % SLOTS) ^ vswz(key)) * 8);
-            __builtin_amdgcn_global_load_lds((vglb_void *)(Kb + ko), (vlds_void *)(kd + (size_t)i * 1024), 16, 0, 2);
-            __builtin_amdgcn_global_load_lds((vglb_void *)(Vb + vo), (vlds_void *)(vd + (size_t)i * 1024), 16, 0, 2);
+            const int i = wave * NLD + u;
+            unsigned ko = koff[u], vo = voff[u];
+            if (!whole) {
+                const int key = (i * 64 + lane) / SLOTS, kc = min(key, hi_b - 1 - jt);
+                ko += (unsigned)((kc - key) * (int)krow); vo += (unsigned)((kc - key) * (int)krow);
+            }
+            __builtin_amdgcn_global_load_lds((vglb_void *)(kt + ko), (vlds_void *)(kd + (size_t)i * 1024), 16, 0, 2);
+            __builtin_amdgcn_global_load_lds((vglb_void *)(vt + vo), (vlds_void *)(vd + (size_t)i * 1024), 16, 0, 2);
         }
     };
 #pragma unroll
     for (int k = 0; k < NS - 1; k++) issue(k);
     // Tile it landed (the min(NS - 2, ntile - 1 - it) younger tiles may still fly).
-    static_assert(NS == 4, "tail waits");
+    static_assert(NS >= 3 && NS <= 6, "tail waits");
     auto wait_tile = [&](int it) {
-        if (it + NS - 2 < ntile) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD * (NS - 2)) : "memory");
-        else if (it + 1 < ntile) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD) : "memory");
+        const int younger = min(NS - 2, ntile - 1 - it);
+        if (younger >= NS - 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD * (NS - 2)) : "memory");
+        else if (younger == 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD * 3) : "memory");
+        else if (younger == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD * 2) : "memory");
+        else if (younger == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NLD) : "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     };
     if (!active) {                // a wave past the last row block only streams its share of the ring
@@ -663,12 +679,17 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
             else s0 = mfma16<F16>(kf[ks], qf[ks], s0);
         }
         const f32x4 sc = (s0 + s1) * a.sl2;
-        const bool full = jt >= j_lo && jt + KT <= j_hi && jt >= lo_max && jt + KT - 1 <= pos_min;
+        // Masks: one wave-uniform test for a tile whose keys every row attends; else per key.
         float tv[4];
+        if (jt >= j_lo && jt + KT <= j_hi && jt >= lo_max && jt + KT - 1 <= pos_min) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int key = jt + 4 * g + i;
-            tv[i] = (full || (key >= j_lo && key < j_hi && rm.attends(key))) ? sc[i] : kNegInf;
+            for (int i = 0; i < 4; i++) tv[i] = sc[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int key = jt + 4 * g + i;
+                tv[i] = (key >= j_lo && key < j_hi && rm.attends(key)) ? sc[i] : kNegInf;
+            }
         }
         float mx = fmaxf(fmaxf(tv[0], tv[1]), fmaxf(tv[2], tv[3]));
         mx = max_over_groups(mx);
