@@ -54,12 +54,14 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// Work split of verify_kernel. The key tiles of every (token tile z, KV head) pair, in the order (z, KV head, tile),
-// are cut into equal runs of q tiles, one run per workgroup of a grid of resident workgroups, so every workgroup
-// streams the same number of bytes whatever the mix of sequence lengths (a grid of fixed key chunks leaves a
-// partly filled last round of workgroups). A run writes one partial per pair it meets, into slot (workgroup index
-// - index of the pair's first workgroup); the last run of a pair marks the slot after its own for the combine. q depends on the
-// total tile count, so verify results depend on the batch; they are deterministic for given inputs.
+// Work split of verify_kernel. Pair z is (sequence, token tile) with n_z key tiles per KV head. The key tiles of one
+// KV head's list (pairs in order) are cut into G / NKV equal runs of q tiles, and every KV head takes the same cut:
+// workgroup w streams run w / NKV of KV head w % NKV. So every workgroup streams the same number of bytes whatever
+// the mix of sequence lengths (a grid of fixed key chunks leaves a partly filled last round of workgroups), and
+// the NKV workgroups that read the head slices of the same key rows run side by side (HBM row locality). A run
+// writes one partial per pair it meets, into slot (run index - index of the pair's first run); the last run of a
+// pair marks the slot after its own for the combine. q depends on the total tile count, so verify results depend
+// on the batch; they are deterministic for given inputs.
 struct SegPair { int seq, tok0, tok1, lo, hi, jb, n; };
 
 __device__ __forceinline__ SegPair seg_pair(const Problem &p, int tpb, int nchunks, int z) {
@@ -85,15 +87,16 @@ __device__ __forceinline__ SegPair seg_pair_u(const Problem &p, int tpb, int nch
     return s;
 }
 
-// Over pairs z = 0 .. nseq * nchunks - 1 (pair z holds NKV * n_z tiles): the total N, the pair zx holding global
-// tile x and the tiles before it px, and the tiles before pair zq (pq). Called by whole waves (wave-uniform).
+// Over pairs z = 0 .. nseq * nchunks - 1 (pair z holds n_z tiles per KV head): the total N, the pair zx holding
+// tile x of one KV head's list and the tiles before it px, and the tiles before pair zq (pq). Called by whole waves
+// (wave-uniform).
 __device__ __forceinline__ void seg_scan(const Problem &p, int tpb, int nchunks, int x, int zq, int &N, int &zx,
                                          int &px, int &pq) {
     const int lane = threadIdx.x & 63, nz = p.nseq * nchunks;
     N = 0; zx = -1; px = 0; pq = 0;
     for (int z0 = 0; z0 < nz; z0 += 64) {
         const int zl = z0 + lane;
-        const int cnt = zl < nz ? p.NKV * seg_pair(p, tpb, nchunks, zl).n : 0;
+        const int cnt = zl < nz ? seg_pair(p, tpb, nchunks, zl).n : 0;
         int incl = cnt;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -576,26 +579,6 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
     const KE *Kb = kv_base<KE>(p, false, seq) + (size_t)kvh * HD;
     const KE *Vb = kv_base<KE>(p, true, seq) + (size_t)kvh * HD;
 
-    // This wave's rows (row block `wave`): Q fragments in registers, the row mask.
-    const int rho = wave * 16 + ln;
-    const bool valid = active && rho < nrows;
-    const int tq = tok0 + (valid ? rho / GRP : 0);
-    u32x4 qf[KS];
-    {
-        const QE *qrow = reinterpret_cast<const QE *>(p.Q) + ((size_t)(seq * p.T + tq) * p.NQ + kvh * GRP + (valid ? rho % GRP : 0)) * HD + 8 * g;
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) qf[ks] = valid ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
-    }
-    RowMask rm;
-    rm.pos = tok_pos(p, seq, tq); rm.lo = win_lo(rm.pos, p.window); rm.valid = valid;
-    rm.tree = p.anc != nullptr; rm.anc = p.anc ? p.anc[seq * p.T + tq] : 0u; rm.tb = p.anc ? tok_pos(p, seq, 0) : 0;
-    int lo_max = 0, pos_min = INT_MAX;
-    for (int t = tok0; t < tok1; t++) {
-        const int ps = tok_pos(p, seq, t);
-        lo_max = max(lo_max, win_lo(ps, p.window)); pos_min = min(pos_min, ps);
-    }
-    if (p.anc) pos_min = min(pos_min, tok_pos(p, seq, 0) - 1);
-
     // Tile k (keys jb + KT k ..) -> stage k % NS. Thread slot S of a tensor's tile holds the 16-byte column
     // (S % SLOTS) ^ swz(key) of key row S / SLOTS (per-thread offsets below; the tile's first row is a scalar);
     // keys past the end re-read the last key (they are masked). Nothing is issued past the segment's last tile
@@ -627,6 +610,27 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
     };
 #pragma unroll
     for (int k = 0; k < NS - 1; k++) issue(k);
+    // This wave's rows (row block `wave`): Q fragments in registers, the row mask (requested after the first tiles,
+    // which therefore leave at once).
+    const int rho = wave * 16 + ln;
+    const bool valid = active && rho < nrows;
+    const int tq = tok0 + (valid ? rho / GRP : 0);
+    u32x4 qf[KS];
+    {
+        const QE *qrow = reinterpret_cast<const QE *>(p.Q) + ((size_t)(seq * p.T + tq) * p.NQ + kvh * GRP + (valid ? rho % GRP : 0)) * HD + 8 * g;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) qf[ks] = valid ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
+    }
+    RowMask rm;
+    rm.pos = tok_pos(p, seq, tq); rm.lo = win_lo(rm.pos, p.window); rm.valid = valid;
+    rm.tree = p.anc != nullptr; rm.anc = p.anc ? p.anc[seq * p.T + tq] : 0u; rm.tb = p.anc ? tok_pos(p, seq, 0) : 0;
+    int lo_max = 0, pos_min = INT_MAX;
+    for (int t = tok0; t < tok1; t++) {
+        const int ps = tok_pos(p, seq, t);
+        lo_max = max(lo_max, win_lo(ps, p.window)); pos_min = min(pos_min, ps);
+    }
+    if (p.anc) pos_min = min(pos_min, tok_pos(p, seq, 0) - 1);
+
     // Tile it landed (the min(NS - 2, ntile - 1 - it) younger tiles may still fly).
     static_assert(NS >= 3 && NS <= 6, "tail waits");
     auto wait_tile = [&](int it) {
@@ -733,28 +737,55 @@ template <int HD, int RB, int KVT, int QT>
 __global__ void __launch_bounds__(256) verify_kernel(const SplitArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const Problem &p = a.p;
-    const int w = blockIdx.x, G = gridDim.x;
+    const int G1 = gridDim.x / p.NKV, run = blockIdx.x / p.NKV, kvh = blockIdx.x % p.NKV;
+    if (run >= G1) return;
+    const int lane = threadIdx.x & 63, nz = p.nseq * a.nchunks;
+    // Up to 64 pairs: lane z holds pair z, so one round of position loads gives the totals, the run's first pair and
+    // every later pair (by lane exchange). More pairs: scans over the positions.
+    const bool small = nz <= 64;
+    const SegPair mine = (small && lane < nz) ? seg_pair(p, a.tpb, a.nchunks, lane) : SegPair{0, 0, 0, 0, 0, 0, 0};
+    auto pair_at = [&](int z) {
+        if (!small) return seg_pair_u(p, a.tpb, a.nchunks, z);
+        SegPair sp;
+        sp.seq = __builtin_amdgcn_readfirstlane(__shfl(mine.seq, z));
+        sp.tok0 = __builtin_amdgcn_readfirstlane(__shfl(mine.tok0, z));
+        sp.tok1 = __builtin_amdgcn_readfirstlane(__shfl(mine.tok1, z));
+        sp.lo = __builtin_amdgcn_readfirstlane(__shfl(mine.lo, z));
+        sp.hi = __builtin_amdgcn_readfirstlane(__shfl(mine.hi, z));
+        sp.jb = __builtin_amdgcn_readfirstlane(__shfl(mine.jb, z));
+        sp.n = __builtin_amdgcn_readfirstlane(__shfl(mine.n, z));
+        return sp;
+    };
+    int incl = mine.n;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+    }
     int N, z, P, pz;
-    seg_scan(p, a.tpb, a.nchunks, INT_MAX, 0, N, z, P, pz);
-    const int q = max((N + G - 1) / G, a.part.seg_qmin);
-    const long long xs = (long long)w * q;
+    if (small) N = __builtin_amdgcn_readfirstlane(__shfl(incl, 63));
+    else seg_scan(p, a.tpb, a.nchunks, INT_MAX, 0, N, z, P, pz);
+    const int q = max((N + G1 - 1) / G1, a.part.seg_qmin);
+    const long long xs = (long long)run * q;
     if (xs >= N) return;
     int x = (int)xs;
     const int x1 = (int)min((long long)N, xs + q);
-    seg_scan(p, a.tpb, a.nchunks, x, 0, N, z, P, pz);
-    SegPair sp = seg_pair_u(p, a.tpb, a.nchunks, z);
+    if (small) {
+        z = __builtin_amdgcn_readfirstlane(__builtin_ctzll(__ballot(incl > x)));
+        P = __builtin_amdgcn_readfirstlane(__shfl(incl, z) - __shfl(mine.n, z));
+    } else {
+        seg_scan(p, a.tpb, a.nchunks, x, 0, N, z, P, pz);
+    }
+    SegPair sp = pair_at(z);
     for (;;) {
-        const int local = x - P, kvh = local / sp.n, t0 = local % sp.n;
-        const int t1 = min(sp.n, t0 + (x1 - x)), slot = w - (P + kvh * sp.n) / q;
-        if (kvh >= p.NKV || slot < 0 || slot >= a.part.ns_cap) break;   // unreachable while the counts agree
+        const int t0 = x - P, t1 = min(sp.n, t0 + (x1 - x)), slot = run - P / q;
+        if (slot < 0 || slot >= a.part.ns_cap) break;     // unreachable while the counts agree
         verify_segment<HD, RB, KVT, QT>(a, sp, kvh, t0, t1, slot, t1 == sp.n, smem);
         x += t1 - t0;
         if (x >= x1) break;
-        if (t1 == sp.n && kvh == p.NKV - 1) {            // next pair (every pair holds at least one tile)
-            P += p.NKV * sp.n;
-            sp = seg_pair_u(p, a.tpb, a.nchunks, ++z);
-        }
-        __syncthreads();                                 // every wave is done with the ring
+        P += sp.n;                                        // next pair (every pair holds at least one tile)
+        sp = pair_at(++z);
+        __syncthreads();                                  // every wave is done with the ring
     }
 }
 
@@ -800,6 +831,7 @@ static hipError_t launch_split_t(SplitArgs &a, dim3 grid, hipStream_t st) {
             // q >= qmin keeps a pair within ns_cap slots: a pair of n <= max_pos/16 + 1 tiles meets at most
             // floor((n - 1) / q) + 2 runs (with fewer than ns_cap, the slot after the last holds the end mark).
             const int nmax = a.p.max_pos / 16 + 1;
+            G = std::max(a.p.NKV, G - G % a.p.NKV);          // the same G / NKV runs for every KV head
             a.part.seg_g = G;
             a.part.seg_qmin = std::max(8, (nmax - 1) / (a.part.ns_cap - 1) + 1);
             hipLaunchKernelGGL((verify_kernel<HD, RB, KVT, QT>), dim3(G), dim3(256), VerifyCfg<HD>::LDS, st, a);
