@@ -55,15 +55,14 @@ struct DecodeCfg {
 // index order and a CU that receives more workgroups than the others shares its bandwidth among them, so the short
 // items go last, where they land on the CUs that get a third workgroup (measured: a CU with three full items runs
 // 20% longer than one with two).
-__device__ __forceinline__ bool find_item(const Problem &p, int C, int &seq, int &c) {
+__device__ __forceinline__ bool find_item(const Problem &p, int C, int &seq, int &c, int &lo, int &hi) {
     const int lane_ = threadIdx.x & 63, cmax = p.max_pos / C;
     int rest = (int)blockIdx.x / p.NKV;
     seq = -1; c = 0;
     for (int phase = 0; phase < 2; phase++) {
         for (int s0 = 0; s0 < p.nseq; s0 += 64) {
-            int n = 0, first = 0;
+            int n = 0, first = 0, lo_s = INT_MAX, hi_s = 0;   // key range of the sequence's tokens
             if (s0 + lane_ < p.nseq) {
-                int lo_s = INT_MAX, hi_s = 0;              // key range of the sequence's tokens
                 for (int t = 0; t < p.T; t++) {
                     const int ps = tok_pos(p, s0 + lane_, t);
                     lo_s = min(lo_s, win_lo(ps, p.window)); hi_s = max(hi_s, ps + 1);
@@ -84,6 +83,7 @@ __device__ __forceinline__ bool find_item(const Problem &p, int C, int &seq, int
                 seq = s0 + l;
                 c = phase == 0 ? __shfl(first, l) + rest - (__shfl(incl, l) - __shfl(m, l))
                                : __shfl(first, l) + __shfl(n, l) - 1;
+                lo = __shfl(lo_s, l); hi = __shfl(hi_s, l);
                 return true;
             }
             rest -= __shfl(incl, 63);
@@ -103,15 +103,12 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
 
     const Problem &p = a.p;
     const int C = a.C;
-    int seq, c;
-    if (!find_item(p, C, seq, c)) return;
+    int seq, c, lo, hi;
+    if (!find_item(p, C, seq, c, lo, hi)) return;
+    seq = __builtin_amdgcn_readfirstlane(seq); c = __builtin_amdgcn_readfirstlane(c);
+    lo = __builtin_amdgcn_readfirstlane(lo); hi = __builtin_amdgcn_readfirstlane(hi);
     const int kvh = (int)blockIdx.x % p.NKV;
     const int GRP = p.NQ / p.NKV, nrows = p.T * GRP;          // rows rho = token-major (token, head)
-    int lo = INT_MAX, hi = 0;
-    for (int t = 0; t < p.T; t++) {
-        const int ps = tok_pos(p, seq, t);
-        lo = min(lo, win_lo(ps, p.window)); hi = max(hi, ps + 1);
-    }
     const int j_lo = max(c * C, lo), j_hi = min(c * C + C, hi);
     if (j_lo >= j_hi) return;
 
@@ -416,15 +413,12 @@ __global__ void __launch_bounds__(128) decode_f32_kernel(const DecodeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const Problem &p = a.p;
     const int C = a.C;
-    int seq, c;
-    if (!find_item(p, C, seq, c)) return;
+    int seq, c, lo, hi;
+    if (!find_item(p, C, seq, c, lo, hi)) return;
+    seq = __builtin_amdgcn_readfirstlane(seq); c = __builtin_amdgcn_readfirstlane(c);
+    lo = __builtin_amdgcn_readfirstlane(lo); hi = __builtin_amdgcn_readfirstlane(hi);
     const int kvh = (int)blockIdx.x % p.NKV;
     const int GRP = p.NQ / p.NKV, nrows = p.T * GRP;
-    int lo = INT_MAX, hi = 0;
-    for (int t = 0; t < p.T; t++) {
-        const int ps = tok_pos(p, seq, t);
-        lo = min(lo, win_lo(ps, p.window)); hi = max(hi, ps + 1);
-    }
     const int j_lo = max(c * C, lo), j_hi = min(c * C + C, hi);
     if (j_lo >= j_hi) return;
 
