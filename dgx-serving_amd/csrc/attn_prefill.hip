@@ -429,7 +429,43 @@ prefill_kernel(const PrefArgs a) {
                 l[rb] += (pv[0] + pv[1]) + (pv[2] + pv[3]);
                 pop[sub][rb] = u32x2{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3])};
             }
-        if constexpr (!MIX) {
+        if constexpr (!MIX && NSUB == 2) {
+            // PV on 16x16x32 over both sub-tiles at once (the order of keys inside an MFMA's reduction is free):
+            // k-group g of the MFMA holds keys 4g..4g+3 of sub-tile 0 and then of sub-tile 1, which is what the
+            // lane's two S^T fragments hold (B operand = the two P^T halves) and what two transpose reads of V give
+            // (A operand). Software-pipelined: batch b = 4 dim blocks (8 reads); batch b+1 is read before batch b's
+            // MFMAs.
+            constexpr int PB = 4, NPB = DB / PB;
+            u32x2 vb2[2][2 * PB];
+            auto rdv = [&](int b, u32x2 (&dst)[2 * PB]) {
+#pragma unroll
+                for (int j = 0; j < PB; j++)
+#pragma unroll
+                    for (int sub = 0; sub < 2; sub++)
+                        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(dst[2 * j + sub])
+                                     : "v"((vbase + sub * 16 * ROWB) ^ (32u * (b * PB + j))) : "memory");
+            };
+            const u32x4 pp = u32x4{pop[0][0][0], pop[0][0][1], pop[1][0][0], pop[1][0][1]};
+            rdv(0, vb2[0]);
+#pragma unroll
+            for (int b = 0; b < NPB; b++) {
+                u32x2 (&cur)[2 * PB] = vb2[b & 1];
+                if (b + 1 < NPB) {
+                    rdv(b + 1, vb2[(b + 1) & 1]);
+                    asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]),
+                                 "+v"(cur[5]), "+v"(cur[6]), "+v"(cur[7])::"memory");
+                } else {
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]),
+                                 "+v"(cur[5]), "+v"(cur[6]), "+v"(cur[7])::"memory");
+                }
+#pragma unroll
+                for (int j = 0; j < PB; j++)
+                    acc[0][b * PB + j] = mfma16<F16>(u32x4{cur[2 * j][0], cur[2 * j][1], cur[2 * j + 1][0], cur[2 * j + 1][1]},
+                                                     pp, acc[0][b * PB + j]);
+                if (pt < NPART && b % 2 == 1) issue_pt(nxt, pt++);
+            }
+        }
+        if constexpr (!MIX && NSUB != 2) {
             // Software-pipelined PV: batch b = 8 dim blocks of one sub-tile; batch b+1 is read before batch b's MFMAs.
             constexpr int PB = 8, NPB = NSUB * DB / PB;
             u32x2 vb2[2][PB];
