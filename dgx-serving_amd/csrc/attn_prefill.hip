@@ -96,11 +96,14 @@ struct PrefCfg {
     static_assert((KG == 2 || KG == 4) && DB % KG == 0, "key groups");
 };
 
-// Slot swizzle of key row k: 16-byte column c of key k sits in slot c ^ swz(k), a permutation of the low 4 key
-// bits (keys 0-7 to the even slots, 8-15 to the odd ones). It spreads the 16 keys of a K fragment read over the
-// 16 slots of a 256-byte bank row, and the 8 keys x 2 columns that the 32 lanes of a half V transpose read
-// (keys 4g..4g+3 for g = 0, 1 or g = 2, 3) over all 16 slots as well.
-__device__ __forceinline__ int swz(int k) { return ((k & 7) << 1) | ((k >> 3) & 1); }
+// Slot swizzles of key row k: 16-byte column c of key k sits in slot c ^ swz(k). V rows use vswz, a permutation of
+// the low 4 key bits (keys 0-7 to the even slots, 8-15 to the odd ones), which spreads the 8 keys x 2 columns that
+// the 32 lanes of a half V transpose read (keys 4g..4g+3 for g = 0, 1 or g = 2, 3) over all 16 slots of a 256-byte
+// bank row. K rows are read 16 bytes per lane by key (lane = key, column 4 ks + g): kswz(k) = k puts the 8 (16)
+// keys of a lane group on distinct bank quads (vswz, with its even slots for keys 0-7, measured 4 conflict cycles
+// per read there).
+__device__ __forceinline__ int vswz(int k) { return ((k & 7) << 1) | ((k >> 3) & 1); }
+__device__ __forceinline__ int kswz(int k) { return k & 15; }
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void glb_void;
@@ -166,13 +169,15 @@ prefill_kernel(const PrefArgs a) {
     const int s0 = j_lo / SK, nsteps = j_lo < j_hi ? (j_hi - 1) / SK - s0 + 1 : 0;
 
     // Step loads: thread slot S = (wave*NLD + u)*64 + lane of the K (V) half of a stage holds the 16-byte column
-    // (S % SLOTS) ^ swz(key) of key row key = S / SLOTS; its byte offset from the step's first key row is fixed.
+    // (S % SLOTS) ^ kswz(key) (vswz(key)) of key row key = S / SLOTS; its byte offset from the step's first key row
+    // is fixed.
     const unsigned krow_b = (unsigned)(krow * sizeof(KE));
-    unsigned ld_off[NLD];
+    unsigned ld_koff[NLD], ld_voff[NLD];
 #pragma unroll
     for (int u = 0; u < NLD; u++) {
         const int S = (wave * NLD + u) * 64 + lane, key = S / SLOTS;
-        ld_off[u] = (unsigned)key * krow_b + (unsigned)(((S % SLOTS) ^ swz(key)) * 8 * sizeof(KE));
+        ld_koff[u] = (unsigned)key * krow_b + (unsigned)(((S % SLOTS) ^ kswz(key)) * 8 * sizeof(KE));
+        ld_voff[u] = (unsigned)key * krow_b + (unsigned)(((S % SLOTS) ^ vswz(key)) * 8 * sizeof(KE));
     }
     // Step k of the walk into stage k % NS. Keys past the last position re-read that position (they are masked), so
     // every load is in bounds; only a step that crosses the end needs the clamped addresses.
@@ -199,17 +204,17 @@ prefill_kernel(const PrefArgs a) {
             if constexpr (!DMA) {
                 const char *ks = reinterpret_cast<const char *>(Kb) + soff;
                 const char *vs = reinterpret_cast<const char *>(Vb) + soff;
-                unsigned off = ld_off[u];
-                if (s * SK + SK > hi_b) {
-                    const unsigned key = off / krow_b, lim = (unsigned)(hi_b - 1 - s * SK);
-                    if (key > lim) off -= (key - lim) * krow_b;
-                }
+                unsigned koff = ld_koff[u], voff = ld_voff[u];
                 const int S = i * 64 + lane;
-                *reinterpret_cast<u32x4 *>(kd + (size_t)S * 16) = load8_op<KVT, F16>(reinterpret_cast<const KE *>(ks + off));
-                *reinterpret_cast<u32x4 *>(vd + (size_t)S * 16) = load8_op<KVT, F16>(reinterpret_cast<const KE *>(vs + off));
+                if (s * SK + SK > hi_b) {
+                    const unsigned key = (unsigned)(S / SLOTS), lim = (unsigned)(hi_b - 1 - s * SK);
+                    if (key > lim) { koff -= (key - lim) * krow_b; voff -= (key - lim) * krow_b; }
+                }
+                *reinterpret_cast<u32x4 *>(kd + (size_t)S * 16) = load8_op<KVT, F16>(reinterpret_cast<const KE *>(ks + koff));
+                *reinterpret_cast<u32x4 *>(vd + (size_t)S * 16) = load8_op<KVT, F16>(reinterpret_cast<const KE *>(vs + voff));
             } else {
-                buffer_load_lds16(krs, kd + (size_t)i * 1024, (int)ld_off[u]);
-                buffer_load_lds16(vrs, vd + (size_t)i * 1024, (int)ld_off[u]);
+                buffer_load_lds16(krs, kd + (size_t)i * 1024, (int)ld_koff[u]);
+                buffer_load_lds16(vrs, vd + (size_t)i * 1024, (int)ld_voff[u]);
             }
         }
     };
@@ -290,8 +295,8 @@ prefill_kernel(const PrefArgs a) {
     // 4g + ln/4 is at vaddr ^ (32 db).
     const unsigned lds0 = (unsigned)(uintptr_t)smem;
     const int vr = 4 * g + (ln >> 2);
-    const unsigned kaddr = lds0 + (kg * Cf::KT + ln) * ROWB + ((g ^ swz(ln)) << 4);
-    const unsigned vaddr = lds0 + Cf::HALF + (kg * Cf::KT + vr) * ROWB + 8 * (ln & 1) + ((((ln & 3) >> 1) ^ swz(vr)) << 4);
+    const unsigned kaddr = lds0 + (kg * Cf::KT + ln) * ROWB + ((g ^ kswz(ln)) << 4);
+    const unsigned vaddr = lds0 + Cf::HALF + (kg * Cf::KT + vr) * ROWB + 8 * (ln & 1) + ((((ln & 3) >> 1) ^ vswz(vr)) << 4);
 
     // One step's work for the row blocks in ACT (a wave-uniform bit mask). QK: the K fragments of a sub-tile are
     // read in batches of 4 k-steps (inline asm, one wait per batch, so the reads are not serialised behind the
