@@ -13,14 +13,15 @@
 //
 // Keys are walked in steps of SK keys at absolute positions; each wave takes the NSUB 16-key sub-tiles of its key
 // group in a step (one wave per key group and row group). K and V of a step go from HBM/L2 straight into LDS
-// with gfx950 direct-to-LDS loads (global_load_lds_dwordx4: no staging registers), NS-stage ring, one barrier
-// per step. The LDS rows are unpadded and their 16-byte slots are XOR-swizzled by the key (swz). Each wave then
+// with gfx950 direct-to-LDS buffer loads (no staging registers; the buffer range makes rows past the last key
+// read as zeros), NS-stage ring, one barrier per step. The LDS rows are unpadded and their 16-byte slots are
+// XOR-swizzled by the key (kswz, vswz). Each wave then
 //   * computes S^T = K Q^T for its rows on 16x16x32 MFMA (K fragments from LDS, Q fragments in registers),
 //   * masks (causal / window; a wave-uniform test picks the unmasked fast path) and runs the online softmax in
 //     registers over all its keys of the step (a row lives in 4 lanes; the running max moves lazily, so the
 //     accumulator is rescaled on few steps),
-//   * computes O^T += V^T P^T on 16x16x16 MFMA with V^T read transposed from LDS (ds_read_b64_tr_b16) and P^T
-//     straight from the softmax registers.
+//   * computes O^T += V^T P^T on 16x16x32 MFMA over its two sub-tiles at once (16x16x16 at HD 512) with V^T
+//     read transposed from LDS (ds_read_b64_tr_b16) and P^T straight from the softmax registers.
 // At the end the two key-group states of each row are merged through LDS.
 //
 // Determinism and chunk invariance: step boundaries are absolute, the key group of a sub-tile depends only on
@@ -55,14 +56,10 @@ struct PrefArgs {
 
 // A workgroup is RG x KG waves. RB: 16-row blocks per wave; RG: row groups (waves splitting the tile's rows); KG:
 // key groups (waves splitting each step's keys); NS: LDS stages; NSUB: 16-key sub-tiles per wave and step.
-// MIX = false: RB = 1, the row groups split the tile's rows (the first half of them on the first half tile).
-// MIX = true: RB = 2, row group rg holds rows [16 rg, 16 rg + 16) of BOTH half tiles (block 0 from the first,
-// block 1 from the second), so in a causal pair every wave works while either half has keys, and a K or V
-// fragment read from LDS serves both blocks.
-template <int HD, int RB, int RG, int KG_, int NS_, int NSUB_, bool MIX_>
+// RB = 1: the row groups split the tile's rows (the first half of them on the first half tile).
+template <int HD, int RB, int RG, int KG_, int NS_, int NSUB_>
 struct PrefCfg {
     static constexpr int KG = KG_, NS = NS_, NW = RG * KG_, NT = NW * 64, NSUB = NSUB_;
-    static constexpr bool MIX = MIX_;
     static constexpr int KT = 16 * NSUB;                 // keys per wave per step (NSUB 16-key sub-tiles)
     static constexpr int SK = KG * KT;                   // keys per step
     static constexpr int RR = RG * RB * 16;              // rows per workgroup tile
@@ -81,17 +78,10 @@ struct PrefCfg {
     static constexpr size_t LDS_MERGE = (size_t)RG * KG * (KG - 1) * 16 * XSTR * 4;
     static constexpr size_t LDS_STATS = (size_t)2 * NW * RB * 16 * 4;
     static constexpr size_t LDS_MAIN = LDS_TILES > LDS_MERGE ? LDS_TILES : LDS_MERGE;
-    // MIX: the Q fragments of both blocks sit in LDS in fragment order [block][row group][k-step][lane] (16 B
-    // each), which keeps the wave within 256 VGPRs (two waves per SIMD); the merge statistics then use the tile
-    // region past the merge exchange (both are needed only after the step loop).
-    static constexpr int QR = MIX ? 0 : RB;              // row blocks whose Q fragments stay in registers
-    static constexpr size_t LDS_Q = MIX ? (size_t)RB * RG * KS * 1024 : 0;
-    static constexpr bool STATS_IN_MAIN = MIX && LDS_MERGE + LDS_STATS <= LDS_MAIN;
-    static constexpr size_t STATS_OFF = STATS_IN_MAIN ? LDS_MERGE : LDS_MAIN;
-    static constexpr size_t LDS = LDS_MAIN + (STATS_IN_MAIN ? 0 : LDS_STATS) + LDS_Q;
-    static constexpr size_t Q_OFF = LDS - LDS_Q;
+    static constexpr size_t STATS_OFF = LDS_MAIN;        // merge statistics past the tiles
+    static constexpr size_t LDS = LDS_MAIN + LDS_STATS;
     static_assert(NLD >= 1 && (SK * SLOTS) % NT == 0, "step loads");
-    static_assert(MIX ? RB == 2 : (RB == 1 && RG % 2 == 0), "row block layout");
+    static_assert(RB == 1 && RG % 2 == 0, "row block layout");
     static_assert(NS >= 2 && NS <= 4, "stages");
     static_assert((KG == 2 || KG == 4) && DB % KG == 0, "key groups");
 };
@@ -116,10 +106,10 @@ __device__ __forceinline__ void wait_steps(int pending) {
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <int HD, int RB, int RG, int KG_, int NS_, int NSUB, bool MIX, int WPE, int KVT, int QT, int OT>
+template <int HD, int RB, int RG, int KG_, int NS_, int NSUB, int WPE, int KVT, int QT, int OT>
 __global__ void __launch_bounds__(RG * KG_ * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 prefill_kernel(const PrefArgs a) {
-    using Cf = PrefCfg<HD, RB, RG, KG_, NS_, NSUB, MIX>;
+    using Cf = PrefCfg<HD, RB, RG, KG_, NS_, NSUB>;
     constexpr int KG = Cf::KG, NS = Cf::NS, SK = Cf::SK, KS = Cf::KS, DB = Cf::DB, NLD = Cf::NLD, DO = Cf::DO;
     constexpr int SLOTS = Cf::SLOTS, ROWB = Cf::ROWB, HR = Cf::HR;
     constexpr bool F16 = OpIsF16<KVT>::value;
@@ -232,16 +222,13 @@ prefill_kernel(const PrefArgs a) {
     int htok[RB], hrows[RB], lrow[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
-        const int hb = MIX ? rb : (rg * 16) / HR;
-        lrow[rb] = MIX ? rg * 16 : rg * 16 - hb * HR;
+        const int hb = (rg * 16) / HR;
+        lrow[rb] = rg * 16 - hb * HR;
         htok[rb] = hb ? tok0[1] : tok0[0];
         hrows[rb] = (hb ? tok1[1] - tok0[1] : tok1[0] - tok0[0]) * GRP;
     }
     int rpos[RB], rlo[RB];
-    constexpr int QR = Cf::QR;
-    u32x4 qop[QR > 0 ? QR : 1][KS];
-    unsigned char *qlds = smem + Cf::Q_OFF;                             // MIX: Q fragments [rb][rg][ks][lane]
-    const unsigned qaddr = (unsigned)(uintptr_t)qlds + (unsigned)(rg * KS * 1024 + lane * 16);
+    u32x4 qop[RB][KS];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
         const int rho = lrow[rb] + ln;
@@ -251,16 +238,8 @@ prefill_kernel(const PrefArgs a) {
         rpos[rb] = valid ? ps : -1;
         rlo[rb] = win_lo(ps, p.window);
         const QE *qrow = reinterpret_cast<const QE *>(p.Q) + ((size_t)(seq * p.T + t) * p.NQ + h) * HD + 8 * g;
-        if (rb < QR) {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                qop[rb < QR ? rb : 0][ks] = valid ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
-        } else if (kg == 0) {                                           // one wave per row group stores them
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                *reinterpret_cast<u32x4 *>(qlds + (size_t)((rb * RG + rg) * KS + ks) * 1024 + lane * 16) =
-                    valid ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
-        }
+        for (int ks = 0; ks < KS; ks++) qop[rb][ks] = valid ? load8_op<QT, F16>(qrow + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
     }
     // Steps 1..NS-2 go out after the Q loads, so that waiting for step it never waits for younger steps.
 #pragma unroll
@@ -306,14 +285,14 @@ prefill_kernel(const PrefArgs a) {
         int pt = 0;
         // Per-lane LDS bases, made opaque so that the XOR-swizzled fragment addresses are formed next to their
         // reads instead of being hoisted out of the step loop (which held ~30 address registers live and spilled).
-        unsigned kbase = kaddr + stage, vbase = vaddr + stage, qbase = qaddr;
-        asm volatile("" : "+v"(kbase), "+v"(vbase), "+v"(qbase));
+        unsigned kbase = kaddr + stage, vbase = vaddr + stage;
+        asm volatile("" : "+v"(kbase), "+v"(vbase));
         f32x4 s[NSUB][RB], s2[NSUB][RB];
 #pragma unroll
         for (int sub = 0; sub < NSUB; sub++)
 #pragma unroll
             for (int rb = 0; rb < RB; rb++) s[sub][rb] = s2[sub][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (!MIX) {
+        {
             // Software-pipelined: batch b = k-steps 2b, 2b+1 of every sub-tile (4 reads at NSUB = 2); batch b+1 is
             // read before batch b's MFMAs, so the LDS latency hides under them (4 independent MFMA chains).
             constexpr int KPB = 2, NB = KS / KPB, RPB = KPB * NSUB;
@@ -353,41 +332,6 @@ prefill_kernel(const PrefArgs a) {
                     }
             }
         }
-        if constexpr (MIX) {
-            // Batches of 2 k-steps: the K fragments of the sub-tile and the Q fragments of each active block (Q
-            // from LDS at constant offsets from one base). Small batches keep the wave within 256 VGPRs; the second
-            // wave on the SIMD covers the read latency.
-#pragma unroll
-            for (int sub = 0; sub < NSUB; sub++) {
-                const unsigned ka = kbase + sub * 16 * ROWB;
-#pragma unroll
-                for (int k2 = 0; k2 < KS; k2 += 2) {
-                    u32x4 kf[2], qf[2][2];
-#pragma unroll
-                    for (int q = 0; q < 2; q++)
-                        asm volatile("ds_read_b128 %0, %1" : "=v"(kf[q]) : "v"(ka ^ (64u * (k2 + q))) : "memory");
-#pragma unroll
-                    for (int rb = 0; rb < RB; rb++) {
-                        if ((ACT >> rb) & 1) {
-#pragma unroll
-                            for (int q = 0; q < 2; q++)
-                                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(qf[rb][q])
-                                             : "v"(qbase), "n"(1024 * ((rb * RG) * KS + k2 + q)) : "memory");
-                        }
-                    }
-                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(kf[0]), "+v"(kf[1]), "+v"(qf[0][0]), "+v"(qf[0][1]),
-                                 "+v"(qf[1][0]), "+v"(qf[1][1])::"memory");
-                    if (k2 == 0 || k2 == KS / 2) issue_pt(nxt, pt++);
-#pragma unroll
-                    for (int rb = 0; rb < RB; rb++) {
-                        if ((ACT >> rb) & 1) {
-#pragma unroll
-                            for (int q = 0; q < 2; q++) s[sub][rb] = mfma16<F16>(kf[q], qf[rb][q], s[sub][rb]);
-                        }
-                    }
-                }
-            }
-        }
         float tv[NSUB][RB][4], mnew[RB];
         bool need = false;
 #pragma unroll
@@ -398,7 +342,7 @@ prefill_kernel(const PrefArgs a) {
             float mx = kNegInf;
 #pragma unroll
             for (int sub = 0; sub < NSUB; sub++) {
-                const f32x4 sc = (RB == 1 ? s[sub][rb] + s2[sub][rb] : s[sub][rb]) * a.sl2;
+                const f32x4 sc = (s[sub][rb] + s2[sub][rb]) * a.sl2;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int key = jw + 16 * sub + 4 * g + i;
@@ -434,7 +378,7 @@ prefill_kernel(const PrefArgs a) {
                 l[rb] += (pv[0] + pv[1]) + (pv[2] + pv[3]);
                 pop[sub][rb] = u32x2{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3])};
             }
-        if constexpr (!MIX && NSUB == 2) {
+        if constexpr (NSUB == 2) {
             // PV on 16x16x32 over both sub-tiles at once (the order of keys inside an MFMA's reduction is free):
             // k-group g of the MFMA holds keys 4g..4g+3 of sub-tile 0 and then of sub-tile 1, which is what the
             // lane's two S^T fragments hold (B operand = the two P^T halves) and what two transpose reads of V give
@@ -470,7 +414,7 @@ prefill_kernel(const PrefArgs a) {
                 if (pt < NPART && b % 2 == 1) issue_pt(nxt, pt++);
             }
         }
-        if constexpr (!MIX && NSUB != 2) {
+        if constexpr (NSUB != 2) {
             // Software-pipelined PV: batch b = 8 dim blocks of one sub-tile; batch b+1 is read before batch b's MFMAs.
             constexpr int PB = 8, NPB = NSUB * DB / PB;
             u32x2 vb2[2][PB];
@@ -495,38 +439,6 @@ prefill_kernel(const PrefArgs a) {
                 const int sub = b / (DB / PB), d0 = (b % (DB / PB)) * PB;
 #pragma unroll
                 for (int j = 0; j < PB; j++) acc[0][d0 + j] = mfma16k16<F16>(cur[j], pop[sub][0], acc[0][d0 + j]);
-                if (pt < NPART && b % 2 == 1) issue_pt(nxt, pt++);
-            }
-        }
-        if constexpr (MIX) {
-            // Software-pipelined PV, double-buffered: batch b = 4 dim blocks of one sub-tile; batch b+1 is read
-            // before batch b's MFMAs.
-            constexpr int PB = 4, NPB = NSUB * DB / PB;
-            u32x2 vb4[2][PB];
-            auto rdv = [&](int b, u32x2 (&dst)[PB]) {
-                const int sub = b / (DB / PB), d0 = (b % (DB / PB)) * PB;
-#pragma unroll
-                for (int j = 0; j < PB; j++)
-                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(dst[j]) : "v"((vbase + sub * 16 * ROWB) ^ (32u * (d0 + j))) : "memory");
-            };
-            rdv(0, vb4[0]);
-#pragma unroll
-            for (int b = 0; b < NPB; b++) {
-                u32x2 (&cur)[PB] = vb4[b & 1];
-                if (b + 1 < NPB) {
-                    rdv(b + 1, vb4[(b + 1) & 1]);
-                    asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3])::"memory");
-                } else {
-                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3])::"memory");
-                }
-                const int sub = b / (DB / PB), d0 = (b % (DB / PB)) * PB;
-#pragma unroll
-                for (int rb = 0; rb < RB; rb++) {
-                    if ((ACT >> rb) & 1) {
-#pragma unroll
-                        for (int j = 0; j < PB; j++) acc[rb][d0 + j] = mfma16k16<F16>(cur[j], pop[sub][rb], acc[rb][d0 + j]);
-                    }
-                }
                 if (pt < NPART && b % 2 == 1) issue_pt(nxt, pt++);
             }
         }
@@ -651,25 +563,23 @@ prefill_kernel(const PrefArgs a) {
 // traffic) as 4 row groups x 2 key groups, 16 rows and HD accumulator columns per wave, a 64-row workgroup tile
 // (two 32-row half tiles), 64-key steps (two 16-key sub-tiles per wave) in two LDS stages. HD 512: 4 waves, a
 // 32-row tile, 32-key steps (a 32-key stage of HD 512 is 64 KB).
-// HD 128/256: 4 waves (2 row groups x 2 key groups) over a 32-row tile with 64 KB of LDS (two stages), so two
-// workgroups share a CU: the L2 -> LDS stream of one 8-wave workgroup with a barrier per step was measured at
-// ~42 B/clk per CU, two 4-wave workgroups at ~57-60 B/clk, and the causal prompt is L2-bandwidth-bound at this
-// size (64 query rows per CU). WPE: waves per SIMD the register allocation must allow. PAIR: whether a
-// workgroup may take the causal half-tile pair (i, n-1-i) (one workgroup per CU) instead of neighbours.
+// Measured alternatives at HD 256 (config 3, T = 1024): 4 waves over a 32-row tile, two workgroups per CU, 38.8
+// vs 30.0 us; 16-key steps per wave, 33.1 us; two 16-row blocks per wave (one wave per SIMD), 36.9 us.
+// WPE: waves per SIMD the register allocation must allow. PAIR: whether a workgroup may take the causal
+// half-tile pair (i, n-1-i) (one workgroup per CU) instead of neighbours.
 template <int HD> struct PrefTile;
-template <> struct PrefTile<128> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 2, WPE = 2; static constexpr bool PAIR = true, MIX = false; };
-template <> struct PrefTile<256> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 2, WPE = 2; static constexpr bool PAIR = true, MIX = false; };
-template <> struct PrefTile<512> { static constexpr int RB = 1, RG = 2, KG = 2, NS = 2, NSUB = 1, WPE = 1; static constexpr bool PAIR = true, MIX = false; };
+template <> struct PrefTile<128> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 2, WPE = 2; static constexpr bool PAIR = true; };
+template <> struct PrefTile<256> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 2, WPE = 2; static constexpr bool PAIR = true; };
+template <> struct PrefTile<512> { static constexpr int RB = 1, RG = 2, KG = 2, NS = 2, NSUB = 1, WPE = 1; static constexpr bool PAIR = true; };
 template <int HD>
-using PrefTileCfg = PrefCfg<HD, PrefTile<HD>::RB, PrefTile<HD>::RG, PrefTile<HD>::KG, PrefTile<HD>::NS, PrefTile<HD>::NSUB,
-                            PrefTile<HD>::MIX>;
+using PrefTileCfg = PrefCfg<HD, PrefTile<HD>::RB, PrefTile<HD>::RG, PrefTile<HD>::KG, PrefTile<HD>::NS, PrefTile<HD>::NSUB>;
 
 template <int HD, int KVT, int QT, int OT>
 static hipError_t launch_pref_t(const PrefArgs &a, dim3 grid, hipStream_t st) {
     using T = PrefTile<HD>;
     using Cf = PrefTileCfg<HD>;
     static bool configured = false;
-    auto kern = prefill_kernel<HD, T::RB, T::RG, T::KG, T::NS, T::NSUB, T::MIX, T::WPE, KVT, QT, OT>;
+    auto kern = prefill_kernel<HD, T::RB, T::RG, T::KG, T::NS, T::NSUB, T::WPE, KVT, QT, OT>;
     if (!configured) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cf::LDS);
