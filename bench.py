@@ -269,7 +269,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "tree", "all"], default="all")
+    ap.add_argument("--only", choices=["decode", "prefill", "tree", "global", "all"], default="all")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (scale reference for HBM byte counters)")
     args = ap.parse_args()
@@ -291,6 +291,15 @@ def main():
         print(json.dumps({"metric": "tree-verify attention GB/s (B16 x 8 draft tokens, L<=16K)",
                           "value": round(tby / (tms * 1e-3) / 1e9, 1), "unit": "GB/s", "us_per_call": round(tms * 1e3, 2),
                           "steps": args.steps, "warmup": args.warmup, "higher_is_better": True}))
+        return
+    if args.only == "global":                 # the Gemma4 global-layer shape alone (profiling); not the headline line
+        gms, gby, gkms = run_global_decode(args.steps, args.warmup)
+        pms2, pfl2 = run_prefill(args.steps, args.warmup, T=1024, NQ=16, NKV=1, HD=512)
+        print(json.dumps({"metric": "Gemma4 global-layer attention (hd 512, 1 KV head)",
+                          "decode_B8": dict(us=round(gms * 1e3, 2), gbs=round(gby / (gms * 1e-3) / 1e9, 1),
+                                            kernel_us=round(gkms * 1e3, 2)),
+                          "prefill_T1024": dict(us=round(pms2 * 1e3, 2), tflops=round(pfl2 / (pms2 * 1e-3) / 1e12, 2)),
+                          "steps": args.steps, "warmup": args.warmup}))
         return
     w = decode_workload()
     ms, nbytes, kms = run_decode(w, args.steps, args.warmup, chunk=int(os.environ.get("BENCH_DECODE_CHUNK", "512")),

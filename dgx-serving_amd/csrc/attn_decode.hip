@@ -37,9 +37,10 @@ struct DecodeCfg {
     static constexpr int NKL = NKL_, RW = RW_, NW = NKL_ * RW_, KT = 16;
     static constexpr int KS = HD / 32;                 // 32-dim blocks (QK k-steps, V fragment loads)
     static constexpr int DB = HD / 16;                 // 16-dim output blocks
-    static constexpr int QSTR = HD + 8;                // Q row stride in LDS (16-bit elements)
+    static constexpr int QSTR = HD + 16;               // Q row stride in LDS (16-bit elements; +16: no bank conflicts)
     static constexpr int BSTR = HD + 4;                // merge buffer row stride (floats)
-    static constexpr int VSTR = HD + 8;                // V tile row stride in LDS (16-bit elements)
+    static constexpr int VSTR = HD + 16;               // V tile row stride in LDS (16-bit elements; +16: the K
+                                                       // fragment and V transpose reads are free of bank conflicts)
     static constexpr int VCH = KT * HD / 8 / 64;       // 16-byte V chunks per lane per tile
     static constexpr size_t LDS_Q = (size_t)RW * 16 * QSTR * 2;
     static constexpr size_t LDS_V = (size_t)NW * KT * VSTR * 2;     // one private tile per wave (K, then V)

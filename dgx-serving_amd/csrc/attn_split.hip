@@ -263,7 +263,8 @@ struct SplitCfg {
     static constexpr int NSUB = KT / 16;
     static constexpr int KS = HD / 32;        // QK k-steps (16x16x32)
     static constexpr int DBW = HD / 16 / NW;  // PV output dim blocks (16x16x16) per wave
-    static constexpr int STR = HD + 8;        // LDS row stride of Q, K and V tiles (16-bit elements)
+    static constexpr int STR = HD + 16;       // LDS row stride of Q, K and V tiles (16-bit elements; +16: the
+                                              // fragment and transpose reads are free of bank conflicts)
     static constexpr int RR = RB * 16;        // query rows per workgroup
     static constexpr int CPT = KT * HD / 8 / (NW * 64);   // 16-byte chunks per thread per tile (K and V each)
     static constexpr int NSTG = 2;                          // register stages of the K/V stream
