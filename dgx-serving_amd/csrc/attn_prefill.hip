@@ -4,9 +4,10 @@
 // runs, flash_attn2bs_p1(_custom)_kernel (kernels/attention_flash.cuh:28-217).
 //
 // Work decomposition. A half tile is 32 rows: tqh tokens x the GRP q-heads of one KV head (token-major), so every
-// K/V byte a workgroup fetches serves the whole GQA group. A workgroup (8 wave64s) takes two half tiles at once and walks the union of their key ranges: for causal prompts the pair
-// (i, n-1-i), so the keys of the short half are fetched once for both and every workgroup carries the same work
-// (a T=1024 prompt at 8 KV heads is 256 equal workgroups); otherwise two neighbouring half tiles. Work items of
+// K/V byte a workgroup fetches serves the whole GQA group. A workgroup (8 wave64s) takes two half tiles at once
+// and walks the union of their key ranges: for causal prompts the pair (i, n-1-i), so the keys of the short half
+// are fetched once for both and every workgroup carries the same work (a T=1024 prompt at 8 KV heads is 256 equal
+// workgroups); otherwise two neighbouring half tiles. Work items of
 // one (sequence, KV head) get consecutive indices and are mapped onto one XCD (workgroups are dispatched
 // round-robin over the 8 XCDs), so that head's K/V stays in one L2.
 //
