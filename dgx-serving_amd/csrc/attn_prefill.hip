@@ -71,7 +71,8 @@ struct PrefCfg {
     static constexpr int ROWB = HD * 2;                  // bytes per key row (16-bit operands)
     static constexpr int HALF = SK * ROWB;               // bytes of one K (or V) step tile
     static constexpr int STAGE = 2 * HALF;               // K and V of one step
-    static constexpr int NLD = SK * SLOTS / NT;          // 16-byte loads per thread per step (K and V each)
+    static constexpr int NLR = SK * SLOTS / 64;          // 64-slot rows of a step tile (one per wave load)
+    static constexpr int NLD = (NLR + NW - 1) / NW;      // 16-byte loads per thread per step (K and V each)
     static constexpr size_t LDS_TILES = (size_t)NS * STAGE;
     static constexpr int XSTR = HD / KG + 4;             // merge exchange row stride (floats)
     // merge exchange of one row block: [row group][owner key group][sender slot (KG-1)][16 rows][XSTR]
@@ -80,7 +81,9 @@ struct PrefCfg {
     static constexpr size_t LDS_MAIN = LDS_TILES > LDS_MERGE ? LDS_TILES : LDS_MERGE;
     static constexpr size_t STATS_OFF = LDS_MAIN;        // merge statistics past the tiles
     static constexpr size_t LDS = LDS_MAIN + LDS_STATS;
-    static_assert(NLD >= 1 && (SK * SLOTS) % NT == 0, "step loads");
+    // Waves past the last 64-slot row issue fewer loads; the step wait is then exact only without younger steps in
+    // flight (NS = 2 waits for vmcnt 0).
+    static_assert((SK * SLOTS) % 64 == 0 && (NLR % NW == 0 || NS == 2), "step loads");
     static_assert(RB == 1 && RG % 2 == 0, "row block layout");
     static_assert(NS >= 2 && NS <= 4, "stages");
     static_assert((KG == 2 || KG == 4) && DB % KG == 0, "key groups");
@@ -191,6 +194,7 @@ prefill_kernel(const PrefArgs a) {
         for (int u = 0; u < NLD; u++) {
             if (u < u0 || u >= u1) continue;
             const int i = wave * NLD + u;
+            if (Cf::NLR % Cf::NW != 0 && i >= Cf::NLR) continue;       // wave-uniform: past the tile
             if constexpr (!DMA) {
                 const char *ks = reinterpret_cast<const char *>(Kb) + soff;
                 const char *vs = reinterpret_cast<const char *>(Vb) + soff;
@@ -567,19 +571,27 @@ prefill_kernel(const PrefArgs a) {
 // two rounds of 256 workgroups: 92 vs 55 us.
 // Measured alternatives at HD 256 (config 3, T = 1024): 4 waves over a 32-row tile, two workgroups per CU, 38.8
 // vs 30.0 us; 16-key steps per wave, 33.1 us; two 16-row blocks per wave (one wave per SIMD), 36.9 us.
+// HD 256, wide tile (W = 1): 12 waves (6 row groups, three per SIMD, 168 VGPRs) over a 96-row tile. Its half tile
+// of 48 rows holds 8 tokens of a 6-head GQA group where the 32-row one holds 5 (30 rows), so the Qwen3.5 prompt
+// (T = 1024, 24 q-heads over 4 KV heads) is 256 workgroups, one round, instead of 412 in two: 53.4 vs 37.2 us. It
+// runs a prompt only when it needs fewer rounds of resident workgroups than the 64-row tile (config 3 is one
+// round either way, and 31.0 vs 35.5 us there). The two tiles share the step (64 keys), the key groups and the
+// merge order, so a row's bits do not depend on which one ran it.
 // WPE: waves per SIMD the register allocation must allow. PAIR: whether a workgroup may take the causal
 // half-tile pair (i, n-1-i) (one workgroup per CU) instead of neighbours.
-template <int HD> struct PrefTile;
-template <> struct PrefTile<128> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 2, WPE = 2; static constexpr bool PAIR = true; };
-template <> struct PrefTile<256> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 2, WPE = 2; static constexpr bool PAIR = true; };
-template <> struct PrefTile<512> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 1, WPE = 2; static constexpr bool PAIR = true; };
-template <int HD>
-using PrefTileCfg = PrefCfg<HD, PrefTile<HD>::RB, PrefTile<HD>::RG, PrefTile<HD>::KG, PrefTile<HD>::NS, PrefTile<HD>::NSUB>;
+template <int HD, int W> struct PrefTile;
+template <> struct PrefTile<128, 0> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 2, WPE = 2; static constexpr bool PAIR = true; };
+template <> struct PrefTile<256, 0> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 2, WPE = 2; static constexpr bool PAIR = true; };
+template <> struct PrefTile<256, 1> { static constexpr int RB = 1, RG = 6, KG = 2, NS = 2, NSUB = 2, WPE = 3; static constexpr bool PAIR = true; };
+template <> struct PrefTile<512, 0> { static constexpr int RB = 1, RG = 4, KG = 2, NS = 2, NSUB = 1, WPE = 2; static constexpr bool PAIR = true; };
+template <int HD, int W>
+using PrefTileCfg = PrefCfg<HD, PrefTile<HD, W>::RB, PrefTile<HD, W>::RG, PrefTile<HD, W>::KG, PrefTile<HD, W>::NS,
+                            PrefTile<HD, W>::NSUB>;
 
-template <int HD, int KVT, int QT, int OT>
+template <int HD, int W, int KVT, int QT, int OT>
 static hipError_t launch_pref_t(const PrefArgs &a, dim3 grid, hipStream_t st) {
-    using T = PrefTile<HD>;
-    using Cf = PrefTileCfg<HD>;
+    using T = PrefTile<HD, W>;
+    using Cf = PrefTileCfg<HD, W>;
     static bool configured = false;
     auto kern = prefill_kernel<HD, T::RB, T::RG, T::KG, T::NS, T::NSUB, T::WPE, KVT, QT, OT>;
     if (!configured) {
@@ -593,29 +605,32 @@ static hipError_t launch_pref_t(const PrefArgs &a, dim3 grid, hipStream_t st) {
 }
 
 template <int KVT, int QT, int OT>
-static hipError_t pref_dispatch_hd(const PrefArgs &a, dim3 grid, hipStream_t st) {
+static hipError_t pref_dispatch_hd(const PrefArgs &a, int wide, dim3 grid, hipStream_t st) {
     switch (a.p.HD) {
-    case 128: return launch_pref_t<128, KVT, QT, OT>(a, grid, st);
-    case 256: return launch_pref_t<256, KVT, QT, OT>(a, grid, st);
-    case 512: return launch_pref_t<512, KVT, QT, OT>(a, grid, st);
+    case 128: return launch_pref_t<128, 0, KVT, QT, OT>(a, grid, st);
+    case 256: return wide ? launch_pref_t<256, 1, KVT, QT, OT>(a, grid, st) : launch_pref_t<256, 0, KVT, QT, OT>(a, grid, st);
+    case 512: return launch_pref_t<512, 0, KVT, QT, OT>(a, grid, st);
     default: return hipErrorInvalidValue;
     }
 }
 
-static int pref_half_rows(int HD) {
+// Per tile shape (head dim, W): rows of a half tile, workgroups resident per CU, and whether it takes causal
+// half-tile pairs. HD 128 and 512 have the one shape.
+struct PrefShape { int hr, per_cu; bool pair; };
+template <int HD, int W> static PrefShape pref_shape_t() {
+    return PrefShape{PrefTileCfg<HD, W>::HR, (int)std::max<size_t>(1, (160u << 10) / PrefTileCfg<HD, W>::LDS),
+                     PrefTile<HD, W>::PAIR};
+}
+static PrefShape pref_shape(int HD, int wide) {
     switch (HD) {
-    case 128: return PrefTileCfg<128>::HR;
-    case 256: return PrefTileCfg<256>::HR;
-    case 512: return PrefTileCfg<512>::HR;
-    default: return 0;
+    case 128: return pref_shape_t<128, 0>();
+    case 256: return wide ? pref_shape_t<256, 1>() : pref_shape_t<256, 0>();
+    case 512: return pref_shape_t<512, 0>();
+    default: return PrefShape{0, 1, false};
     }
 }
-// Workgroups of the tile shape resident per CU, and whether it takes causal half-tile pairs.
-static int pref_per_cu(int HD) {
-    const size_t lds = HD == 128 ? PrefTileCfg<128>::LDS : HD == 256 ? PrefTileCfg<256>::LDS : PrefTileCfg<512>::LDS;
-    return (int)std::max<size_t>(1, (160u << 10) / lds);
-}
-static bool pref_pair(int HD) { return HD == 128 ? PrefTile<128>::PAIR : HD == 256 ? PrefTile<256>::PAIR : PrefTile<512>::PAIR; }
+static int pref_half_rows(int HD) { return pref_shape(HD, 0).hr; }
+static int pref_per_cu(int HD) { return pref_shape(HD, 0).per_cu; }
 
 // Key split for kv_split = -1: when the unsplit grid would fill at most half of the workgroup slots (a short run
 // of queries over a long cached prefix), cut the keys into as many absolute splits as whole grids fit on them.
@@ -639,32 +654,42 @@ int prefill_auto_split(const Problem &p) {
 
 hipError_t launch_prefill(const Problem &p, int kv_split, const Partials &part, hipStream_t st) {
     if (p.NQ % p.NKV || p.anc || p.pos_mode != 1) return hipErrorInvalidValue;
-    const int GRP = p.NQ / p.NKV, HR = pref_half_rows(p.HD);
-    if (HR == 0 || GRP > HR) return hipErrorInvalidValue;
+    const int GRP = p.NQ / p.NKV;
+    if (pref_half_rows(p.HD) == 0 || GRP > pref_half_rows(p.HD)) return hipErrorInvalidValue;
     if (kv_split < 0 || (kv_split > 0 && kv_split % 64)) return hipErrorInvalidValue;
-    const int tqh = HR / GRP;
-    const int nht = (p.T + tqh - 1) / tqh;
     const int nsplit = kv_split > 0 ? p.max_pos / kv_split + 1 : 1;
     if (kv_split > 0 && nsplit > part.ns_cap) return hipErrorInvalidValue;
-    // Pair half tiles (i, n-1-i) when causal work varies across the prompt (no window, prefix shorter than the
-    // chunk); otherwise a workgroup takes two neighbouring half tiles.
-    const int pair = (pref_pair(p.HD) && kv_split == 0 && p.window == 0 && nht >= 2 && p.max_pos < 2 * p.T) ? 1 : 0;
-    const int nitems = ((nht + 1) / 2) * nsplit;
-    const long nwg = (long)p.nseq * p.NKV * nitems;
-    if (nwg <= 0 || nwg > (1L << 30)) return hipErrorInvalidConfiguration;
     int dev = 0, ncu = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         ncu = 0;
-    const int fold = (pref_per_cu(p.HD) >= 2 && nwg <= (long)pref_per_cu(p.HD) * ncu) ? 1 : 0;
+    // Workgroups of a tile shape: half tiles of tqh tokens, two per workgroup.
+    auto wgs = [&](const PrefShape &sh) { return (long)p.nseq * p.NKV * (((p.T + sh.hr / GRP - 1) / (sh.hr / GRP) + 1) / 2); };
+    auto rounds = [&](const PrefShape &sh) { const long slots = (long)std::max(ncu, 1) * sh.per_cu; return (wgs(sh) + slots - 1) / slots; };
+    // The wide HD 256 tile, when it takes fewer rounds of resident workgroups (unsplit prompts, 16-bit caches: the
+    // fp32 cache's register staging spills in it).
+    int wide = 0;
+    if (p.HD == 256 && kv_split == 0 && p.kv_dtype != DT_FP32 && ncu > 0 && GRP <= pref_shape(256, 1).hr &&
+        rounds(pref_shape(256, 1)) < rounds(pref_shape(256, 0)))
+        wide = 1;
+    const PrefShape sh = pref_shape(p.HD, wide);
+    const int tqh = sh.hr / GRP;
+    const int nht = (p.T + tqh - 1) / tqh;
+    // Pair half tiles (i, n-1-i) when causal work varies across the prompt (no window, prefix shorter than the
+    // chunk); otherwise a workgroup takes two neighbouring half tiles.
+    const int pair = (sh.pair && kv_split == 0 && p.window == 0 && nht >= 2 && p.max_pos < 2 * p.T) ? 1 : 0;
+    const int nitems = ((nht + 1) / 2) * nsplit;
+    const long nwg = (long)p.nseq * p.NKV * nitems;
+    if (nwg <= 0 || nwg > (1L << 30)) return hipErrorInvalidConfiguration;
+    const int fold = (sh.per_cu >= 2 && nwg <= (long)sh.per_cu * ncu) ? 1 : 0;
     PrefArgs a{p, part, kv_split, nht, nsplit, tqh, pair, nitems, (int)nwg, p.scale * kLog2e, fold};
     dim3 grid((unsigned)(8 * ((nwg + 7) / 8)));
     hipError_t e = hipErrorInvalidValue;
     const int kv = p.kv_dtype, q = p.q_dtype, o = p.o_dtype;
-    if (kv == DT_F16 && q == DT_FP32 && o == DT_FP32) e = pref_dispatch_hd<DT_F16, DT_FP32, DT_FP32>(a, grid, st);
-    else if (kv == DT_BF16 && q == DT_FP32 && o == DT_FP32) e = pref_dispatch_hd<DT_BF16, DT_FP32, DT_FP32>(a, grid, st);
-    else if (kv == DT_FP32 && q == DT_FP32 && o == DT_FP32) e = pref_dispatch_hd<DT_FP32, DT_FP32, DT_FP32>(a, grid, st);
-    else if (kv == DT_F16 && q == DT_F16 && o == DT_F16) e = pref_dispatch_hd<DT_F16, DT_F16, DT_F16>(a, grid, st);
-    else if (kv == DT_BF16 && q == DT_BF16 && o == DT_BF16) e = pref_dispatch_hd<DT_BF16, DT_BF16, DT_BF16>(a, grid, st);
+    if (kv == DT_F16 && q == DT_FP32 && o == DT_FP32) e = pref_dispatch_hd<DT_F16, DT_FP32, DT_FP32>(a, wide, grid, st);
+    else if (kv == DT_BF16 && q == DT_FP32 && o == DT_FP32) e = pref_dispatch_hd<DT_BF16, DT_FP32, DT_FP32>(a, wide, grid, st);
+    else if (kv == DT_FP32 && q == DT_FP32 && o == DT_FP32) e = pref_dispatch_hd<DT_FP32, DT_FP32, DT_FP32>(a, wide, grid, st);
+    else if (kv == DT_F16 && q == DT_F16 && o == DT_F16) e = pref_dispatch_hd<DT_F16, DT_F16, DT_F16>(a, wide, grid, st);
+    else if (kv == DT_BF16 && q == DT_BF16 && o == DT_BF16) e = pref_dispatch_hd<DT_BF16, DT_BF16, DT_BF16>(a, wide, grid, st);
     else return hipErrorInvalidValue;
     if (e != hipSuccess || kv_split <= 0) return e;
     return launch_combine(p, kv_split, part, st);

@@ -91,11 +91,13 @@ def test_config4_sliding_prefill():
     _check(O, qv, k, v, _sample_tokens(Sq, 0, W), Sq, 0, NQ, NKV, HD, "config4 sliding", window=W)
 
 
-@pytest.mark.parametrize("shape", [("sliding", 256, 16, 8, 1024), ("full", 512, 16, 1, 0)])
+@pytest.mark.parametrize("shape", [("sliding", 256, 16, 8, 1024), ("full", 512, 16, 1, 0), ("gqa6", 256, 24, 4, 0)])
 @pytest.mark.parametrize("sq,base", [(1, 0), (6, 1024), (17, 0), (512, 1024), (1024, 0), (2048, 8192)])
 def test_flash_v2_gate(shape, sq, base):
     """tests/test_flash_v2.cu gate: f16 cache (engine default), fp32 Q/O, normalised max error; 30-run
-    determinism; the last rows launched alone equal the full launch bit for bit."""
+    determinism; the last rows launched alone equal the full launch bit for bit. The GQA-6 prompt of 1024 tokens
+    runs on the wide 96-row tile (one round of workgroups) and its last rows alone on the 64-row one, so the
+    bitwise check there also pins that the tile choice leaves a row's bits unchanged."""
     name, HD, NQ, NKV, window = shape
     uq = oracle.gen_lcg(2101 + HD * 17 + sq * 43 + base * 59, sq * NQ * HD)[0]
     q = uq
