@@ -339,6 +339,9 @@ def main():
         pms2, pfl2 = run_prefill(args.steps, args.warmup, T=1024, NQ=16, NKV=1, HD=512)
         extra["prefill_global_hd512_T1024"] = dict(us=round(pms2 * 1e3, 2), tflops=round(pfl2 / (pms2 * 1e-3) / 1e12, 2),
                                                    frac_bf16_peak=round(pfl2 / (pms2 * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
+        qms, qfl = run_prefill(args.steps, args.warmup, T=1024, NQ=24, NKV=4, HD=256)   # Qwen3.5 full-attention shape
+        extra["prefill_qwen35_gqa6_T1024"] = dict(us=round(qms * 1e3, 2), tflops=round(qfl / (qms * 1e-3) / 1e12, 2),
+                                                  frac_bf16_peak=round(qfl / (qms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
     out = {
         "metric": "decode-attn HBM GB/s (B16 ragged <=8K) + prefill-attn TFLOP/s (T=1024)",
         "value": round(gbs, 1),
