@@ -348,13 +348,21 @@ prefill_kernel(const PrefArgs a) {
             for (int sub = 0; sub < NSUB; sub++) {
                 const f32x4 sc = (s[sub][rb] + s2[sub][rb]) * a.sl2;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int key = jw + 16 * sub + 4 * g + i;
-                    const bool in = full || (key >= j_lo && key < j_hi && key >= rlo[rb] && key <= rpos[rb]);
-                    tv[sub][rb][i] = in ? sc[i] : kNegInf;
-                    mx = fmaxf(mx, tv[sub][rb][i]);
-                }
+                for (int i = 0; i < 4; i++) tv[sub][rb][i] = sc[i];
             }
+            if (!full) {                                        // one wave-uniform test; per key only off the fast path
+#pragma unroll
+                for (int sub = 0; sub < NSUB; sub++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int key = jw + 16 * sub + 4 * g + i;
+                        if (!(key >= j_lo && key < j_hi && key >= rlo[rb] && key <= rpos[rb])) tv[sub][rb][i] = kNegInf;
+                    }
+            }
+#pragma unroll
+            for (int sub = 0; sub < NSUB; sub++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) mx = fmaxf(mx, tv[sub][rb][i]);
             mx = max_over_groups(mx);
             if (mx > m[rb] + kRescaleThreshold) { mnew[rb] = mx; need = true; }
         }
