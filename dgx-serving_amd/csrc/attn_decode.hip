@@ -492,9 +492,13 @@ __global__ void __launch_bounds__(128) decode_f32_kernel(const DecodeArgs a) {
         float tv[4];
         const bool full = jt >= j_lo && jt + KT <= j_hi && jt >= lo_max && jt + KT - 1 <= pos_min;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int key = jt + 4 * g + i;
-            tv[i] = (full || ((key >= j_lo) & (key < j_hi) & rm.attends(key))) ? sc[i] : kNegInf;
+        for (int i = 0; i < 4; i++) tv[i] = sc[i];
+        if (!full) {                                            // one wave-uniform test; per key only off the fast path
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int key = jt + 4 * g + i;
+                if (!((key >= j_lo) & (key < j_hi) & rm.attends(key))) tv[i] = kNegInf;
+            }
         }
         float mx = fmaxf(fmaxf(tv[0], tv[1]), fmaxf(tv[2], tv[3]));
         mx = max_over_groups(mx);

@@ -445,12 +445,21 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
             for (int sub = 0; sub < NSUB; sub++) {
                 const f32x4 sc = s[sub][rb] + s2[sub][rb];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int key = jt + 16 * sub + 4 * g + i;
-                    const float v = (full || (key >= j_lo && key < j_hi && rm[rb].attends(key))) ? sc[i] * a.sl2 : kNegInf;
-                    tv[sub][rb][i] = v; mx = fmaxf(mx, v);
-                }
+                for (int i = 0; i < 4; i++) tv[sub][rb][i] = sc[i] * a.sl2;
             }
+            if (!full) {                                        // one wave-uniform test; per key only off the fast path
+#pragma unroll
+                for (int sub = 0; sub < NSUB; sub++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int key = jt + 16 * sub + 4 * g + i;
+                        if (!(key >= j_lo && key < j_hi && rm[rb].attends(key))) tv[sub][rb][i] = kNegInf;
+                    }
+            }
+#pragma unroll
+            for (int sub = 0; sub < NSUB; sub++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) mx = fmaxf(mx, tv[sub][rb][i]);
             mx = max_over_groups(mx);
             if (mx > m[rb] + kRescaleThreshold) { mnew[rb] = mx; need = true; } else mnew[rb] = m[rb];
         }
