@@ -182,14 +182,22 @@ prefill_kernel(const PrefArgs a) {
     int it_cur = 0;                                                     // the step being computed
     // Step k < 0 is a no-op step: every lane is out of range, so its loads write zeros into the stage of the step
     // before (already consumed by every wave) and touch no memory; this keeps the issue points branch-free.
-    auto issue_part = [&](int k, int u0, int u1) {
-        const int s = s0 + (k < 0 ? 0 : k);
-        unsigned char *kd = smem + (size_t)((k < 0 ? it_cur + 1 : k) % NS) * Cf::STAGE, *vd = kd + Cf::HALF;
-        const int soff = __builtin_amdgcn_readfirstlane(key_row(p, s * SK) * (int)krow_b);
+    // prep(k) forms a step's buffer descriptors and stage once; issue_part(st, u0, u1) issues slots [u0, u1).
+    struct StepLd { __amdgpu_buffer_rsrc_t krs, vrs; unsigned char *kd; int s, soff; };
+    auto prep = [&](int k) {
+        StepLd st;
+        st.s = s0 + (k < 0 ? 0 : k);
+        st.kd = smem + (size_t)((k < 0 ? it_cur + 1 : k) % NS) * Cf::STAGE;
+        st.soff = __builtin_amdgcn_readfirstlane(key_row(p, st.s * SK) * (int)krow_b);
         // the step's rows as the buffer (the range check covers the vector offset only)
-        const uint32_t left = k < 0 || (uint32_t)soff >= kv_bytes ? 0u : kv_bytes - (uint32_t)soff;
-        const __amdgpu_buffer_rsrc_t krs = make_rsrc(reinterpret_cast<const char *>(Kb) + soff, left);
-        const __amdgpu_buffer_rsrc_t vrs = make_rsrc(reinterpret_cast<const char *>(Vb) + soff, left);
+        const uint32_t left = k < 0 || (uint32_t)st.soff >= kv_bytes ? 0u : kv_bytes - (uint32_t)st.soff;
+        st.krs = make_rsrc(reinterpret_cast<const char *>(Kb) + st.soff, left);
+        st.vrs = make_rsrc(reinterpret_cast<const char *>(Vb) + st.soff, left);
+        return st;
+    };
+    auto issue_part = [&](const StepLd &st, int u0, int u1) {
+        const int s = st.s, soff = st.soff;
+        unsigned char *kd = st.kd, *vd = kd + Cf::HALF;
 #pragma unroll
         for (int u = 0; u < NLD; u++) {
             if (u < u0 || u >= u1) continue;
@@ -207,17 +215,17 @@ prefill_kernel(const PrefArgs a) {
                 *reinterpret_cast<u32x4 *>(kd + (size_t)S * 16) = load8_op<KVT, F16>(reinterpret_cast<const KE *>(ks + koff));
                 *reinterpret_cast<u32x4 *>(vd + (size_t)S * 16) = load8_op<KVT, F16>(reinterpret_cast<const KE *>(vs + voff));
             } else {
-                buffer_load_lds16(krs, kd + (size_t)i * 1024, (int)ld_koff[u]);
-                buffer_load_lds16(vrs, vd + (size_t)i * 1024, (int)ld_voff[u]);
+                buffer_load_lds16(st.krs, kd + (size_t)i * 1024, (int)ld_koff[u]);
+                buffer_load_lds16(st.vrs, vd + (size_t)i * 1024, (int)ld_voff[u]);
             }
         }
     };
-    auto issue = [&](int k) { issue_part(k, 0, NLD); };
+    auto issue = [&](int k) { issue_part(prep(k), 0, NLD); };
     // The next step's loads go out in four parts spread over the current step (between the QK batches, after
     // the softmax, between the PV batches): a workgroup's 8 waves issuing all of them at once stalled every wave
     // on the vector memory pipe for about a thousand cycles per step.
     constexpr int NPART = 4, PPART = (NLD + NPART - 1) / NPART;
-    auto issue_pt = [&](int k, int pt) { issue_part(k, pt * PPART, min(NLD, (pt + 1) * PPART)); };
+    auto issue_pt = [&](const StepLd &st, int pt) { issue_part(st, pt * PPART, min(NLD, (pt + 1) * PPART)); };
     if (nsteps > 0) issue(0);
 
     // This wave's row blocks: block rb covers rows [lrow[rb], lrow[rb] + 16) of half tile hb[rb]. Q fragments and
@@ -285,7 +293,7 @@ prefill_kernel(const PrefArgs a) {
     // read in batches of 4 k-steps (inline asm, one wait per batch, so the reads are not serialised behind the
     // MFMAs) and each active row block runs its MFMA chain on them. Then one softmax update, then PV with V^T
     // fragments in batches of 8 transpose reads. A block left out keeps its state exactly (it attends no key).
-    auto step = [&](const int ACT, int jw, unsigned stage, int nxt) {
+    auto step = [&](const int ACT, int jw, unsigned stage, const StepLd &nxt) {
         int pt = 0;
         // Per-lane LDS bases, made opaque so that the XOR-swizzled fragment addresses are formed next to their
         // reads instead of being hoisted out of the step loop (which held ~30 address registers live and spilled).
@@ -480,7 +488,7 @@ prefill_kernel(const PrefArgs a) {
         int act = 0;                                                    // wave-uniform mask of active row blocks
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) act |= (jw > whi[rb] || jw + Cf::KT - 1 < wlo[rb]) ? 0 : 1 << rb;
-        step(RB == 1 ? 1 : __builtin_amdgcn_readfirstlane(act), jw, stage, nxt);
+        step(RB == 1 ? 1 : __builtin_amdgcn_readfirstlane(act), jw, stage, prep(nxt));
     }
     for (; it < nsteps; it++) issue(sync_step(it));
     // The no-op loads of the last steps still write (zeros) into a stage: drain them before the merge reuses the
