@@ -190,6 +190,25 @@ def run_kv_append(steps, warmup, B=16, T=1, NKV=4, HD=256, ML=8192, kvdt=1):
     return fused, looped, B * T * row * (4 + 2) * 2
 
 
+def run_norm_rope(steps, warmup, T=1024, NKV=8, HD=256):
+    """Gemma4 k append of a T-token prompt chunk: per-head RMSNorm + RoPE + bf16 store into the cache (one
+    dgx_norm_rope_store launch, launch_norm_rope_store's k call of models/gemma4_decode.cu:354). Returns (ms,
+    algorithmic bytes: the fp32 rows and weights read, one cos and one sin half-row per token, the bf16 rows
+    written)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    rows = T * NKV
+    g = torch.Generator(device="cuda").manual_seed(11)
+    X = torch.randn(rows * HD, device="cuda", generator=g)
+    W = torch.randn(HD, device="cuda", generator=g)
+    c, s_ = oracle.rope_tables(T, HD)
+    C, S = torch.from_numpy(c).cuda(), torch.from_numpy(s_).cuda()
+    Kc = torch.zeros(T * NKV * HD, device="cuda", dtype=torch.bfloat16)
+    ms = timed(lambda: A.norm_rope_store(X, W, Kc, 2, rows, NKV, HD, 1e-6, C, S, base=0, pos_step=1, slot_stride=0,
+                                         row_stride=NKV * HD, rope=True), steps, warmup)
+    return ms, rows * HD * (4 + 2) + HD * 4 + T * HD * 4
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -330,6 +349,8 @@ def main():
         ams, lms, aby = run_kv_append(args.steps, args.warmup)
         extra["kv_append_B16"] = dict(us=round(ams * 1e3, 2), per_slot_loop_us=round(lms * 1e3, 2),
                                       gbs=round(aby / (ams * 1e-3) / 1e9, 1))
+        nms, nby = run_norm_rope(args.steps, args.warmup)
+        extra["norm_rope_store_T1024"] = dict(us=round(nms * 1e3, 2), gbs=round(nby / (nms * 1e-3) / 1e9, 1))
         tms, tby = run_tree(args.steps, args.warmup)
         extra["tree_verify_B16x8"] = dict(us=round(tms * 1e3, 2), gbs=round(tby / (tms * 1e-3) / 1e9, 1))
         gms, gby, gkms = run_global_decode(args.steps, args.warmup)

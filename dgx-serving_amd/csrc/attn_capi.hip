@@ -410,6 +410,15 @@ hipError_t dgx_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int
 }
 hipError_t dgx_kv_stats(unsigned out[4]) { return read_kv_stats(out); }
 
+hipError_t dgx_norm_rope_store(const float *X, const float *W, void *Y, int y_dtype, int rows, int NH, int hd, float eps,
+                               const float *cosT, const float *sinT, int base, int pos_step, const int *pos_arr,
+                               long slot_stride, long row_stride, int rope, hipStream_t st) {
+    if (rows == 0) return hipSuccess;
+    if (!valid_dtype(y_dtype)) return hipErrorInvalidValue;
+    return launch_norm_rope_store(X, W, Y, y_dtype, rows, NH, hd, eps, cosT, sinT, base, pos_step, pos_arr, slot_stride,
+                                  row_stride, rope != 0, st);
+}
+
 hipError_t dgx_kv_append(const float *k_src, const float *v_src, void *Kc, void *Vc, int kv_dtype, int nseq, int T,
                          long kv_stride, int row_elems, const int *pos_b, int base, hipStream_t st) {
     if (nseq == 0 || T == 0) return hipSuccess;

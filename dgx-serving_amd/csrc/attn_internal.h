@@ -99,5 +99,9 @@ hipError_t launch_kv_store(const float *src, void *dst, size_t n, int kv_dtype, 
 hipError_t launch_kv_append(const float *ks, const float *vs, void *Kc, void *Vc, int kv_dtype, int nseq, int T,
                             long kv_stride, int row, const int *pos_b, int base, int stats, hipStream_t st);
 hipError_t read_kv_stats(unsigned out[4]);
+bool norm_rope_shape_ok(int hd, bool rope);
+hipError_t launch_norm_rope_store(const float *X, const float *W, void *Y, int y_dtype, int rows, int NH, int hd,
+                                  float eps, const float *cosT, const float *sinT, int base, int pos_step,
+                                  const int *pos_arr, long slot_stride, long row_stride, bool rope, hipStream_t st);
 
 }  // namespace dgx

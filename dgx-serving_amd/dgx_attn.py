@@ -43,6 +43,7 @@ def lib():
             "dgx_kv_store": ([P, P, S, I, I, P], I),
             "dgx_kv_stats": ([P], I),
             "dgx_kv_append": ([P, P, P, P, I, I, I, L64, I, P, I, P], I),
+            "dgx_norm_rope_store": ([P, P, P, I, I, I, I, F, P, P, I, I, P, L64, L64, I, P], I),
             "dgx_attn_batch": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, P, I, I, P, F, I], I),
             "dgx_attn_batch_noalloc": ([P, I, P, P, I, P, I, P, I, I, I, I, I, P, I, L64, P, I, I, P, F, I], I),
             "dgx_attn_batch_ex": ([P, I, P, P, P, P, I, P, I, P, P, I, I, I, I, I, I, P, I, L64, P, I, I, P, F, I, I], I),
@@ -141,6 +142,14 @@ def kv_store(src, dst, n, kv_dtype, which):
 def kv_append(k_src, v_src, Kc, Vc, kv_dtype, nseq, T, kv_stride, row_elems, pos_b=None, base=0):
     _ck(lib().dgx_kv_append(_ptr(k_src), _ptr(v_src), _ptr(Kc), _ptr(Vc), kv_dtype, nseq, T, kv_stride, row_elems,
                             _ptr(pos_b), base, _stream()), "dgx_kv_append")
+
+
+def norm_rope_store(X, W, Y, y_dtype, rows, NH, hd, eps, cosT=None, sinT=None, base=0, pos_step=0, pos_arr=None,
+                    slot_stride=0, row_stride=0, rope=True):
+    """Per-head RMSNorm (+ RoPE) (+ store) of launch_norm_rope_store (kernels/norm_fused.cuh:127-133)."""
+    _ck(lib().dgx_norm_rope_store(_ptr(X), _ptr(W), _ptr(Y), y_dtype, rows, NH, hd, float(eps), _ptr(cosT), _ptr(sinT),
+                                  base, pos_step, _ptr(pos_arr), slot_stride, row_stride, 1 if rope else 0, _stream()),
+        "dgx_norm_rope_store")
 
 
 def kv_stats():

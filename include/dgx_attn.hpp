@@ -58,6 +58,17 @@ static inline void kv_append(const float *k, const float *v, float *Kc, float *V
                       "kv_append");
 }
 
+// ---- kernels/norm_fused.cuh:127-133: per-head RMSNorm (+ RoPE) (+ store in TO = float, __half or __hip_bfloat16)
+template <typename TO>
+static inline void launch_norm_rope_store(const float *X, const float *W, TO *Y, int rows, int NH, int hd, float eps,
+                                          const float *cosT, const float *sinT, int base, int pos_step,
+                                          const int *pos_arr, long slot_stride, long row_stride, bool rope,
+                                          hipStream_t s = 0) {
+    dgx_detail::check(dgx_norm_rope_store(X, W, Y, dgx_detail::kv_code<TO>(), rows, NH, hd, eps, cosT, sinT, base,
+                                          pos_step, pos_arr, slot_stride, row_stride, rope ? 1 : 0, s),
+                      "norm_rope_store");
+}
+
 // ---- kernels/attention.cuh:72-198 (fp32 caches)
 static inline void launch_attn(const float *Q, const float *K, const float *V, float *O, int S, int NQ, int NKV, int HD,
                                hipStream_t st = 0, float scale = 0.f, int window = 0) {

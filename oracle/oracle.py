@@ -169,3 +169,36 @@ def attention_split(q, k, v, kv_off, pos, NQ, NKV, HD, C, scale=0.0, window=0):
     if rc:
         raise ValueError("oracle_attention_split: bad arguments")
     return out, lse
+
+
+def rope_tables(maxpos, hd, theta=10000.0):
+    """cos/sin tables [maxpos, hd] in fp32 as the reference's gates build them (tests/test_norm_fused.cu:90-95):
+    angle p * theta^(-2i/hd) for i < hd/2, written to entries i and hd/2 + i."""
+    p = np.arange(maxpos, dtype=np.float32)[:, None]
+    i = np.arange(hd // 2, dtype=np.float32)[None, :]
+    a = (p * np.power(np.float32(theta), np.float32(-2.0) * i / np.float32(hd))).astype(np.float32)
+    c, s = np.cos(a).astype(np.float32), np.sin(a).astype(np.float32)
+    return np.concatenate([c, c], axis=1), np.concatenate([s, s], axis=1)
+
+
+def norm_rope_rows(x, W, eps, cosT=None, sinT=None, pos=None, rope=True):
+    """Per-head RMSNorm (+ rotate-half RoPE) of the rows x [rows, hd] in float64, restating norm_rope_store_kernel
+    (kernels/norm_fused.cuh:84-126): y = x * (1 / sqrt(sum(x^2) / hd + eps)) * W (norm_par_sumsq / norm_par_mul,
+    :34-52; W None: no scale), then for e < hd/2 with c = cosT[p, e], s = sinT[p, e] (:111-118):
+    o_e = y_e c - y_{e+hd/2} s and o_{e+hd/2} = y_{e+hd/2} c + y_e s. pos[r] is row r's position."""
+    x = np.asarray(x, np.float64)
+    rows, hd = x.shape
+    inv = 1.0 / np.sqrt((x * x).sum(axis=1, keepdims=True) / hd + eps)
+    y = x * inv
+    if W is not None:
+        y = y * np.asarray(W, np.float64)[None, :]
+    if not rope:
+        return y
+    h = hd // 2
+    p = np.asarray(pos, np.int64)
+    c = np.asarray(cosT, np.float64)[p, :h]
+    s = np.asarray(sinT, np.float64)[p, :h]
+    o = np.empty_like(y)
+    o[:, :h] = y[:, :h] * c - y[:, h:] * s
+    o[:, h:] = y[:, h:] * c + y[:, :h] * s
+    return o

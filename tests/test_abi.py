@@ -123,6 +123,10 @@ int main() {
         launch_flash_attn_v2(q, kh, kh, o, 1024, 16, 8, 256, 0, 0, 0.f, 1024, true);
         reserve_flash_attn_scratch(1000, 256);
         kv_store(q, o, 16, 0);
+        // kernels/norm_fused.cuh:127-133 as models/gemma4_decode.cu:353-354 call it (k with RoPE, v without scale)
+        launch_norm_rope_store<__hip_bfloat16>(q, q, const_cast<__hip_bfloat16 *>(kb), 8, 8, 256, 1e-6f, q, q, 100, 1,
+                                               nullptr, 0, 8L * 256, true);
+        launch_norm_rope_store<float>(q, nullptr, o, 8, 8, 256, 1e-6f, q, q, 100, 1, nullptr, 0, 8L * 256, false);
     }
     float *cache = reinterpret_cast<float *>(0x1000);
     printf("%d %d %d %zu %td\n", g4_kv_dtype(), attn_split_chunk(), attn_split_ns_cap(8192), g4_kv_elem(),

@@ -241,3 +241,49 @@ def test_normal_generator_statistics_and_slicing():
     assert np.array_equal(oracle.gen_normal(9, 100, 0.0, 0.5, offset=1000), x[1000:1100])
     u = oracle.gen_uniform_int(4, 256, 8192, 10000)
     assert u.min() >= 256 and u.max() <= 8192 and abs(u.mean() - 4224) < 80
+
+
+# ---- per-head RMSNorm + RoPE (kernels/norm_fused.cuh:84-126): pinned by identities that do not restate it ----
+
+def test_norm_rope_oracle_rms_identities():
+    """RMS step: y = x * sqrt(hd) / sqrt(||x||^2 + hd*eps) (the 2-norm form), a constant row c maps to
+    c / sqrt(c^2 + eps) per element, and W scales elementwise."""
+    rng = np.random.default_rng(5)
+    hd, eps = 64, 1e-6
+    x = rng.standard_normal((5, hd)) * 3.0
+    y = oracle.norm_rope_rows(x, None, eps, rope=False)
+    ref = x * np.sqrt(hd) / np.sqrt(np.linalg.norm(x, axis=1, keepdims=True) ** 2 + hd * eps)
+    assert np.allclose(y, ref, rtol=1e-13, atol=0)
+    c = np.full((1, hd), -2.5)
+    assert np.allclose(oracle.norm_rope_rows(c, None, eps, rope=False), -2.5 / np.sqrt(6.25 + eps), rtol=1e-14)
+    W = rng.standard_normal(hd)
+    assert np.allclose(oracle.norm_rope_rows(x, W, eps, rope=False), y * W[None, :], rtol=1e-14)
+
+
+def test_norm_rope_oracle_rope_is_a_complex_rotation():
+    """Rotate-half RoPE is the complex product (y_e + i y_{e+h}) * (c_e + i s_e): pins the signs and the index
+    pairing; position 0 (angle 0) is the identity and every pair keeps its norm."""
+    rng = np.random.default_rng(6)
+    hd, eps, h = 32, 1e-6, 16
+    cosT, sinT = oracle.rope_tables(40, hd)
+    x = rng.standard_normal((7, hd))
+    pos = np.array([0, 1, 5, 9, 17, 33, 39])
+    y = oracle.norm_rope_rows(x, None, eps, rope=False)
+    o = oracle.norm_rope_rows(x, None, eps, cosT, sinT, pos, rope=True)
+    z = (y[:, :h] + 1j * y[:, h:]) * (cosT[pos, :h].astype(np.float64) + 1j * sinT[pos, :h].astype(np.float64))
+    assert np.allclose(o[:, :h], z.real, rtol=0, atol=1e-13) and np.allclose(o[:, h:], z.imag, rtol=0, atol=1e-13)
+    assert np.array_equal(o[0], y[0])                                  # cos 0 = 1, sin 0 = 0
+    cs2 = cosT[pos, :h].astype(np.float64) ** 2 + sinT[pos, :h].astype(np.float64) ** 2
+    assert np.allclose(o[:, :h] ** 2 + o[:, h:] ** 2, (y[:, :h] ** 2 + y[:, h:] ** 2) * cs2, rtol=1e-12)
+
+
+def test_rope_tables_follow_the_reference_angles():
+    """Table entries are cos/sin of p * 10000^(-2i/hd), duplicated into both halves (tests/test_norm_fused.cu:90-95)."""
+    import math
+    hd = 256
+    cosT, sinT = oracle.rope_tables(4200, hd)
+    for p, i in ((0, 0), (1, 0), (7, 3), (4100, 127), (4199, 64)):
+        a = p * 10000.0 ** (-2.0 * i / hd)
+        for t, f in ((cosT, math.cos), (sinT, math.sin)):
+            assert abs(float(t[p, i]) - f(a)) < 2e-3 + 1e-6 * abs(a)   # fp32 angle rounding at large p
+            assert t[p, i] == t[p, hd // 2 + i]
