@@ -288,7 +288,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "tree", "global", "all"], default="all")
+    ap.add_argument("--only", choices=["decode", "prefill", "tree", "global", "norm", "all"], default="all")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (scale reference for HBM byte counters)")
     args = ap.parse_args()
@@ -305,6 +305,12 @@ def main():
         for _ in range(5):
             dst.copy_(src)
         torch.cuda.synchronize()
+    if args.only == "norm":                   # the norm + RoPE + cache store alone (profiling); not the headline line
+        nms, nby = run_norm_rope(args.steps, args.warmup)
+        print(json.dumps({"metric": "norm+RoPE+store GB/s (1024 tokens x 8 kv heads, hd 256, bf16 cache)",
+                          "value": round(nby / (nms * 1e-3) / 1e9, 1), "unit": "GB/s", "us_per_call": round(nms * 1e3, 2),
+                          "bytes": nby, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True}))
+        return
     if args.only == "tree":                   # the tree-verify workload alone (profiling); not the headline line
         tms, tby = run_tree(args.steps, args.warmup)
         print(json.dumps({"metric": "tree-verify attention GB/s (B16 x 8 draft tokens, L<=16K)",

@@ -38,34 +38,42 @@ __global__ void __launch_bounds__(256) norm_rope_store_kernel(const float *X, co
     if (r >= rows) return;                                             // wave-uniform
     const int s = r / NH, h = r % NH, n4 = hd >> 2;
     const float *xr = X + (size_t)r * hd;
-    f32x4 v[NV];
-    float ss = 0.f;
+    const long p = pos_arr ? (long)pos_arr[s] : (long)base + (long)s * pos_step;
+    // every load of the row goes out before any arithmetic: x, the scale W and this lane's cos / sin entries
+    // (element e takes table entry e mod hd/2; four consecutive elements, one 16-byte load each)
+    const int half = hd >> 1;
+    f32x4 v[NV], wv[NV], cv[NV], sv[NV];
 #pragma unroll
     for (int k = 0; k < NV; k++) {
         const int c = lane + 64 * k;
-        v[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+        v[k] = wv[k] = cv[k] = sv[k] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (c < n4) {
             v[k] = *reinterpret_cast<const f32x4 *>(xr + 4 * c);
-            ss += v[k].x * v[k].x; ss += v[k].y * v[k].y; ss += v[k].z * v[k].z; ss += v[k].w * v[k].w;
+            if (W) wv[k] = *reinterpret_cast<const f32x4 *>(W + 4 * c);
+            if constexpr (ROPE) {
+                const int t = (4 * c) % half;
+                cv[k] = *reinterpret_cast<const f32x4 *>(cosT + p * hd + t);
+                sv[k] = *reinterpret_cast<const f32x4 *>(sinT + p * hd + t);
+            }
         }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+        ss += v[k].x * v[k].x; ss += v[k].y * v[k].y; ss += v[k].z * v[k].z; ss += v[k].w * v[k].w;
     }
     ss = wave_sum64(ss);
     const float inv = rsqrtf(ss / (float)hd + eps);
     f32x4 y[NV];
 #pragma unroll
-    for (int k = 0; k < NV; k++) {
-        const int c = lane + 64 * k;
+    for (int k = 0; k < NV; k++)
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const float t = __fmul_rn(v[k][q], inv);
-            y[k][q] = (W && c < n4) ? __fmul_rn(t, W[4 * c + q]) : t;
+            y[k][q] = W ? __fmul_rn(t, wv[k][q]) : t;
         }
-    }
-    const long p = pos_arr ? (long)pos_arr[s] : (long)base + (long)s * pos_step;
     f32x4 o[NV];
     if constexpr (ROPE) {
-        const int half = hd >> 1;
-        const float *cr = cosT + p * hd, *sr = sinT + p * hd;
 #pragma unroll
         for (int k = 0; k < NV; k++) {
             f32x4 pr;                                                  // the partner chunk's values
@@ -77,21 +85,11 @@ __global__ void __launch_bounds__(256) norm_rope_store_kernel(const float *X, co
 #pragma unroll
                 for (int q = 0; q < 4; q++) pr[q] = __shfl_xor(y[0][q], m);
             }
-            const int c = lane + 64 * k;
-            o[k] = y[k];
-            if (c >= n4) continue;                                     // no element of the row (and no table read)
+            const bool lo = 4 * (lane + 64 * k) < half;                // the chunk lies in one half (half % 4 == 0)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int e = 4 * c + q;
-                if (e < half) {
-                    const float cs = cr[e], sn = sr[e];
-                    o[k][q] = __fsub_rn(__fmul_rn(y[k][q], cs), __fmul_rn(pr[q], sn));
-                } else {
-                    const int j = e - half;
-                    const float cs = cr[j], sn = sr[j];
-                    o[k][q] = __fadd_rn(__fmul_rn(y[k][q], cs), __fmul_rn(pr[q], sn));
-                }
-            }
+            for (int q = 0; q < 4; q++)
+                o[k][q] = lo ? __fsub_rn(__fmul_rn(y[k][q], cv[k][q]), __fmul_rn(pr[q], sv[k][q]))
+                             : __fadd_rn(__fmul_rn(y[k][q], cv[k][q]), __fmul_rn(pr[q], sv[k][q]));
         }
     } else {
 #pragma unroll
