@@ -45,11 +45,11 @@ def _check(out, ref, ydt, what):
         assert not bad.any(), f"{what}: {int(bad.sum())} elements off by more than one 16-bit ulp"
 
 
-@pytest.mark.parametrize("hd", [128, 256, 512])
+@pytest.mark.parametrize("hd", [64, 128, 256, 512, 1024])
 @pytest.mark.parametrize("ydt", [0, 1, 2])
 def test_kv_append_layout_decode(hd, ydt):
     """k (norm + RoPE) and v (norm only) of Sq tokens at base .. base+Sq-1 into one sequence's cache."""
-    nkv = 1 if hd == 512 else 8
+    nkv = 1 if hd >= 512 else 8
     Sq, base, L = 5, 4100, 4200
     rows = Sq * nkv
     x, w, cosT, sinT = _inputs(11 + hd + ydt, rows, hd, L)
