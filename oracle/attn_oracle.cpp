@@ -317,4 +317,31 @@ int oracle_attention_split(const float *q, const float *k, const float *v, const
     return 0;
 }
 
+// Per-head RMSNorm (+ rotate-half RoPE) of rows x [rows, hd] in fp64, restating norm_rope_store_kernel
+// (kernels/norm_fused.cuh:84-126): y = x / sqrt(sum(x^2) / hd + eps) * W (W null: no scale; :34-52), then with
+// c = cosT[p * hd + e], s = sinT[p * hd + e] for e < hd / 2 and p = pos[r] (:111-118):
+// o_e = y_e c - y_{e+hd/2} s, o_{e+hd/2} = y_{e+hd/2} c + y_e s. rope = 0: o = y.
+int oracle_norm_rope(const float *x, const float *W, int rows, int hd, float eps, const float *cosT,
+                     const float *sinT, const int *pos, int rope, double *out) {
+    if (rows < 0 || hd <= 0 || (rope && (hd % 2 || !cosT || !sinT || !pos))) return -1;
+    std::vector<double> y(hd);
+    for (int r = 0; r < rows; r++) {
+        const float *xr = x + (size_t)r * hd;
+        double ss = 0;
+        for (int e = 0; e < hd; e++) ss += (double)xr[e] * xr[e];
+        const double inv = 1.0 / std::sqrt(ss / hd + (double)eps);
+        for (int e = 0; e < hd; e++) y[e] = (double)xr[e] * inv * (W ? (double)W[e] : 1.0);
+        double *o = out + (size_t)r * hd;
+        if (!rope) { for (int e = 0; e < hd; e++) o[e] = y[e]; continue; }
+        const int h = hd / 2;
+        const float *cr = cosT + (size_t)pos[r] * hd, *sr = sinT + (size_t)pos[r] * hd;
+        for (int e = 0; e < h; e++) {
+            const double c = cr[e], sn = sr[e];
+            o[e] = y[e] * c - y[e + h] * sn;
+            o[e + h] = y[e + h] * c + y[e] * sn;
+        }
+    }
+    return 0;
+}
+
 }  // extern "C"

@@ -47,6 +47,8 @@ def lib():
         L.oracle_attention.restype = I
         L.oracle_attention_split.argtypes = [P, P, P, P, P, I, I, I, I, F, I, I, P, P]
         L.oracle_attention_split.restype = I
+        L.oracle_norm_rope.argtypes = [P, P, I, I, F, P, P, P, I, P]
+        L.oracle_norm_rope.restype = I
         _lib = L
     return _lib
 

@@ -12,6 +12,10 @@
 //                                                   bit 32 and beyond are never attended
 //   v2      tests/test_flash_v2.cu                  launch_flash_attn_v2<bf16> chunked prefill with a window
 //   fp32    tests/test_decode_kernels.cu:24-35      launch_attn_decode (Sq > 1, base > 0) at HD 128/256/512
+//   norm    tests/test_norm_fused.cu                launch_norm_rope_store<float / __half / __hip_bfloat16>: the
+//                                                   norm alone at the gate's 1e-6 relative bar, a row's bits
+//                                                   independent of the row count (S = 1..16), and K rows stored
+//                                                   into a 16-bit cache slice within one unit in the last place
 //
 // Expected values come from the CPU oracle (oracle/liboracle.so), which is test infrastructure. Bars: the
 // reference's fp32 bar (error / sum_j p_j |V_j,d| < 1e-5) for fp32 caches and fp32 launchers
@@ -23,6 +27,7 @@
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
+#include <type_traits>
 #include <vector>
 
 extern "C" {
@@ -32,6 +37,10 @@ void oracle_round_bf16(const float *src, float *dst, uint16_t *bits, size_t n);
 int oracle_attention(const float *q, const float *k, const float *v, const long *kv_off, const int *pos,
                      const uint32_t *anc, const int *tree_base, int T, int NQ, int NKV, int HD, float scale,
                      int window, int mode, double *out, double *lse, int nthreads);
+int oracle_norm_rope(const float *x, const float *W, int rows, int hd, float eps, const float *cosT,
+                     const float *sinT, const int *pos, int rope, double *out);
+float oracle_f16_to_f32(uint16_t h);
+float oracle_bf16_to_f32(uint16_t h);
 }
 
 static void ck(hipError_t e) { if (e != hipSuccess) throw std::runtime_error(hipGetErrorString(e)); }
@@ -272,6 +281,107 @@ static void gate_fp32_decode(int HD, int Sq, int base) {
     ck(hipFree(dq)); ck(hipFree(dk)); ck(hipFree(dv)); ck(hipFree(dout));
 }
 
+// RoPE tables [maxpos, hd] as the reference's gate builds them (tests/test_norm_fused.cu:90-95): angle
+// p * 10000^(-2i/hd) in fp32, cos / sin written to entries i and hd/2 + i.
+static void rope_tables(int maxpos, int hd, std::vector<float> &c, std::vector<float> &s) {
+    c.assign((size_t)maxpos * hd, 0.f); s.assign((size_t)maxpos * hd, 0.f);
+    for (int p = 0; p < maxpos; p++)
+        for (int i = 0; i < hd / 2; i++) {
+            const float a = (float)p * powf(10000.f, -2.f * (float)i / (float)hd);
+            c[(size_t)p * hd + i] = c[(size_t)p * hd + hd / 2 + i] = cosf(a);
+            s[(size_t)p * hd + i] = s[(size_t)p * hd + hd / 2 + i] = sinf(a);
+        }
+}
+
+// launch_norm_rope_store gates (tests/test_norm_fused.cu): q rows of S tokens at base .. base+S-1 into scratch
+// (slot stride NQ*hd, row stride 0), k rows of the same tokens into a 16-bit cache slice (slot stride 0, row
+// stride NKV*hd), the norm alone into fp32.
+template <class TO> static bool store_k16(int hd, int NKV, int S, int base, int L, const float *dx, const float *dw,
+                                          const float *dc, const float *ds, const std::vector<double> &ref) {
+    const size_t n = (size_t)L * NKV * hd;
+    std::vector<uint16_t> init(n, 0x7fffu);                           // sentinel: a NaN pattern in both formats
+    uint16_t *dcache = dev(init);
+    launch_norm_rope_store<TO>(dx, dw, reinterpret_cast<TO *>(dcache), S * NKV, NKV, hd, 1e-6f, dc, ds, base, 1,
+                               nullptr, 0, (long)NKV * hd, true);
+    ck(hipDeviceSynchronize());
+    std::vector<uint16_t> h(n);
+    ck(hipMemcpy(h.data(), dcache, n * 2, hipMemcpyDeviceToHost));
+    ck(hipFree(dcache));
+    const bool f16 = std::is_same<TO, __half>::value;
+    const double ulp = f16 ? 1.0 / 1024 : 1.0 / 128, tiny = f16 ? 6.103515625e-05 : 1.1754943508222875e-38;
+    bool ok = true;
+    for (size_t i = 0; i < n; i++) {
+        const size_t row = i / ((size_t)NKV * hd);
+        if (row < (size_t)base || row >= (size_t)(base + S)) { ok &= h[i] == 0x7fffu; continue; }
+        const double r = ref[i - (size_t)base * NKV * hd];
+        const double v = f16 ? oracle_f16_to_f32(h[i]) : oracle_bf16_to_f32(h[i]);
+        ok &= std::fabs(v - r) <= ulp * std::max(std::fabs(r), tiny) + 1e-6;
+    }
+    return ok;
+}
+
+static void gate_norm(int hd) {
+    const int NQ = 16, NKV = hd >= 512 ? 1 : 8, S = 16, base = 4100, L = 4200;
+    const float eps = 1e-6f;
+    uint64_t st = 4242 + hd;
+    std::vector<float> x = xs(st, (size_t)S * NQ * hd, 2.f), w = xs(st, hd), c, s;
+    rope_tables(L, hd, c, s);
+    float *dx = dev(x), *dw = dev(w), *dc = dev(c), *ds = dev(s), *dy;
+    ck(hipMalloc(&dy, x.size() * 4));
+    char what[96];
+    // 1. the norm alone (fp32), relative error < 1e-6 where |ref| >= 1e-3 (tests/test_norm_fused.cu:32-56)
+    launch_norm_rope_store<float>(dx, dw, dy, S * NQ, NQ, hd, eps, nullptr, nullptr, 0, 0, nullptr, (long)NQ * hd, 0,
+                                  false);
+    ck(hipDeviceSynchronize());
+    std::vector<float> y = down(dy, x.size());
+    std::vector<double> ref(x.size());
+    oracle_norm_rope(x.data(), w.data(), S * NQ, hd, eps, nullptr, nullptr, nullptr, 0, ref.data());
+    double worst = 0;
+    for (size_t i = 0; i < y.size(); i++)
+        if (std::fabs(ref[i]) >= 1e-3) worst = std::max(worst, std::fabs(y[i] - ref[i]) / std::fabs(ref[i]));
+    Err e; e.max = worst;
+    snprintf(what, sizeof what, "norm alone hd=%d rel < 1e-6", hd);
+    report("NORM", what, worst < 1e-6, e);
+    // 2. q rows with RoPE for S = 1..16 tokens ending at the same token: that token's rows bit-identical in every
+    //    launch, and the full launch against the oracle
+    std::vector<int> pos(S * NQ);
+    for (int r = 0; r < S * NQ; r++) pos[r] = base + r / NQ;
+    std::vector<double> qref(x.size());
+    oracle_norm_rope(x.data(), w.data(), S * NQ, hd, eps, c.data(), s.data(), pos.data(), 1, qref.data());
+    std::vector<uint32_t> last;
+    bool ident = true;
+    double qmax = 0;
+    for (int n = 1; n <= S; n++) {
+        const int s0 = S - n;
+        launch_norm_rope_store<float>(dx + (size_t)s0 * NQ * hd, dw, dy, n * NQ, NQ, hd, eps, dc, ds, base + s0, 1,
+                                      nullptr, (long)NQ * hd, 0, true);
+        ck(hipDeviceSynchronize());
+        const std::vector<float> o = down(dy, (size_t)n * NQ * hd);
+        std::vector<uint32_t> b(NQ * hd);
+        for (int i = 0; i < NQ * hd; i++) b[i] = bits(o[(size_t)(n - 1) * NQ * hd + i]);
+        if (n == 1) last = b; else ident &= b == last;
+        if (n == S) {
+            double scale = 0;
+            for (double v : qref) scale = std::max(scale, std::fabs(v));
+            for (size_t i = 0; i < o.size(); i++) qmax = std::max(qmax, std::fabs(o[i] - qref[i]) / scale);
+        }
+    }
+    e.max = qmax;
+    snprintf(what, sizeof what, "q norm+RoPE hd=%d S=1..16 row identity, normalised err < 1e-5", hd);
+    report("NORM", what, ident && qmax < 1e-5, e);
+    // 3. k rows (NKV heads) into f16 and bf16 cache slices at rows base .. base+S-1, nothing else written
+    std::vector<int> kpos(S * NKV);
+    for (int r = 0; r < S * NKV; r++) kpos[r] = base + r / NKV;
+    std::vector<double> kref((size_t)S * NKV * hd);
+    oracle_norm_rope(x.data(), w.data(), S * NKV, hd, eps, c.data(), s.data(), kpos.data(), 1, kref.data());
+    const bool k16 = store_k16<__half>(hd, NKV, S, base, L, dx, dw, dc, ds, kref);
+    const bool kb16 = store_k16<__hip_bfloat16>(hd, NKV, S, base, L, dx, dw, dc, ds, kref);
+    e.max = 0;
+    snprintf(what, sizeof what, "k norm+RoPE+store hd=%d f16 / bf16 within 1 ulp, other rows untouched", hd);
+    report("NORM", what, k16 && kb16, e);
+    ck(hipFree(dx)); ck(hipFree(dw)); ck(hipFree(dc)); ck(hipFree(ds)); ck(hipFree(dy));
+}
+
 int main(int argc, char **argv) try {
     setvbuf(stdout, nullptr, _IOLBF, 0);
     const char *only = argc > 1 ? argv[1] : "all";
@@ -293,6 +403,8 @@ int main(int argc, char **argv) try {
         reserve_flash_attn_scratch(4096, 512);          // the fp32 MFMA kernel once its partials are reserved
         for (int hd : {128, 256}) gate_fp32_decode(hd, 6, 1200);
     }
+    if (all || !strcmp(only, "norm"))
+        for (int hd : {128, 256, 512}) gate_norm(hd);
     printf("[ref_gates] %s\n", g_fails ? "FAIL" : "PASS");
     return g_fails ? 1 : 0;
 } catch (const std::exception &e) {

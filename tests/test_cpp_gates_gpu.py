@@ -3,7 +3,7 @@ under the reference's own launcher names (launch_attn_decode_split, launch_flash
 launch_flash_attn_v2<bf16>, launch_attn_decode, attn_split_reserve, kv_at ...), as the reference's
 tests/test_attn_decode_split.cu:58-125 main does, and checks every output against the CPU oracle (gate 1 over
 lengths to 32768, the full gate-2 sweep of 5 bases x S=2..16 and 12 batch widths, a 40-node tree verify, chunked
-prefill and the fp32 decode launcher). The program is built by __graft_entry__.build()."""
+prefill, the fp32 decode launcher and launch_norm_rope_store<float / __half / __hip_bfloat16>). The program is built by __graft_entry__.build()."""
 import os
 import subprocess
 
@@ -36,3 +36,7 @@ def test_split_gates_reference_chunk():
 def test_tree_prefill_fp32_through_cpp_launchers():
     for part in ("tree", "prefill", "fp32"):
         _run(part, {})
+
+
+def test_norm_rope_store_through_cpp_launcher():
+    _run("norm", {})

@@ -128,3 +128,32 @@ def test_rejects_unsupported_shapes():
         A.norm_rope_store(X, None, Y, 0, 4, 4, 96, EPS, X, X, rope=True)
     A.norm_rope_store(X, None, Y, 0, 4, 4, 96, EPS, rope=False)         # plain norm: any hd % 4 == 0
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("hd", [256, 512])
+def test_norm_only_reference_accuracy_bar(hd):
+    """Norm alone into fp32 at the reference gate's accuracy bar (tests/test_norm_fused.cu:32-56): relative error
+    below 1e-6 on every element of magnitude at least 1e-3, against the fp64 oracle."""
+    rows = 64
+    x, w, _, _ = _inputs(71 + hd, rows, hd, 1)
+    Y = torch.empty(rows * hd, device="cuda")
+    A.norm_rope_store(dev(x), dev(w), Y, 0, rows, 1, hd, EPS, rope=False, slot_stride=hd, row_stride=0)
+    torch.cuda.synchronize()
+    ref = oracle.norm_rope_rows(x, w, EPS, rope=False)
+    out = Y.cpu().numpy().astype(np.float64).reshape(rows, hd)
+    big = np.abs(ref) >= 1e-3
+    rel = np.abs(out - ref)[big] / np.abs(ref)[big]
+    assert rel.max() < 1e-6, f"max relative error {rel.max():.3e}"
+
+
+def test_all_tokens_at_one_position():
+    """pos_step 0: every token of the launch takes position base (the rope_partial_batch form of the reference's
+    gate, tests/test_norm_fused.cu:104-105)."""
+    NQ, hd, S, base, L = 8, 256, 5, 777, 1024
+    x, w, cosT, sinT = _inputs(81, S * NQ, hd, L)
+    Y = torch.empty(S * NQ * hd, device="cuda")
+    A.norm_rope_store(dev(x), dev(w), Y, 0, S * NQ, NQ, hd, EPS, dev(cosT), dev(sinT), base=base, pos_step=0,
+                      slot_stride=NQ * hd, row_stride=0, rope=True)
+    torch.cuda.synchronize()
+    ref = oracle.norm_rope_rows(x, w, EPS, cosT, sinT, np.full(S * NQ, base), rope=True)
+    _check(Y.cpu().numpy().reshape(S * NQ, hd), ref, 0, "pos_step 0")

@@ -287,3 +287,24 @@ def test_rope_tables_follow_the_reference_angles():
         for t, f in ((cosT, math.cos), (sinT, math.sin)):
             assert abs(float(t[p, i]) - f(a)) < 2e-3 + 1e-6 * abs(a)   # fp32 angle rounding at large p
             assert t[p, i] == t[p, hd // 2 + i]
+
+
+def test_norm_rope_c_restatement_matches_the_pinned_one():
+    """The C restatement (oracle_norm_rope, which the C++ gate program checks against) agrees with the fp64 numpy
+    restatement pinned above, with and without RoPE and the weight row, at hd 8 .. 512."""
+    import ctypes
+    L = oracle.lib()
+    rng = np.random.default_rng(8)
+    for hd in (8, 64, 256, 512):
+        rows = 9
+        x = (rng.standard_normal((rows, hd)) * 2).astype(np.float32)
+        W = rng.standard_normal(hd).astype(np.float32)
+        cosT, sinT = oracle.rope_tables(300, hd)
+        pos = rng.integers(0, 300, size=rows).astype(np.int32)
+        for w, rope in ((W, True), (None, True), (W, False), (None, False)):
+            out = np.zeros((rows, hd), np.float64)
+            p = lambda a: None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+            rc = L.oracle_norm_rope(p(x), p(w), rows, hd, 1e-6, p(cosT), p(sinT), p(pos), 1 if rope else 0, p(out))
+            assert rc == 0
+            ref = oracle.norm_rope_rows(x, w, 1e-6, cosT, sinT, pos, rope=rope)
+            assert np.allclose(out, ref, rtol=1e-13, atol=1e-13), (hd, w is None, rope)
