@@ -10,10 +10,11 @@
 //   * RMS: each lane sums the squares of its chunks in order, the wave adds the 64 lane sums with a fixed
 //     butterfly; the order depends only on hd, so a row's bits do not depend on how many rows share the launch.
 //     inv = rsqrt(ss / hd + eps); y = (x * inv) * W (two roundings, as the reference's norm_par_mul).
-//   * RoPE (rotate-half): element e < hd/2 pairs with e + hd/2. For hd >= 512 the partner chunk sits in the same
-//     lane (chunk index + hd/512); for hd <= 256 it sits in lane l ^ (hd/8), one cross-lane swap. The products
-//     and the difference / sum are rounded separately: o = t1*c - t2*s, o' = t2*c + t1*s with cos/sin from the
-//     row p of the tables (entries [p*hd, p*hd + hd/2)).
+//   * RoPE (rotate-half): element e < hd/2 pairs with e + hd/2. For hd 512 and 1024 the partner chunk sits in the
+//     same lane (chunk index + hd/512); for power-of-two hd up to 256 it sits in lane l ^ (hd/8), one cross-lane
+//     swap; any other hd (a multiple of 4) takes its partners from the row staged in the wave's LDS slice. The
+//     products and the difference / sum are rounded separately: o = t1*c - t2*s, o' = t2*c + t1*s with cos/sin
+//     from the row p of the tables (entries [p*hd, p*hd + hd/2)).
 //   * Store: p = pos_arr ? pos_arr[s] : base + s * pos_step, row at Y + s*slot_stride + p*row_stride + h*hd, in
 //     fp32 or rounded to nearest-even f16 / bf16 (as kv_store_kernel converts).
 #include "attn_device.h"
@@ -28,7 +29,7 @@ __device__ __forceinline__ float wave_sum64(float v) {
     return v;
 }
 
-template <int DT, bool ROPE, int NV>
+template <int DT, bool ROPE, int NV, bool GEN = false>
 __global__ void __launch_bounds__(256) norm_rope_store_kernel(const float *X, const float *W, void *Y, int rows, int NH,
                                                               int hd, float eps, const float *cosT, const float *sinT,
                                                               int base, int pos_step, const int *pos_arr,
@@ -50,10 +51,18 @@ __global__ void __launch_bounds__(256) norm_rope_store_kernel(const float *X, co
         if (c < n4) {
             v[k] = *reinterpret_cast<const f32x4 *>(xr + 4 * c);
             if (W) wv[k] = *reinterpret_cast<const f32x4 *>(W + 4 * c);
-            if constexpr (ROPE) {
+            if constexpr (ROPE && !GEN) {
                 const int t = (4 * c) % half;
                 cv[k] = *reinterpret_cast<const f32x4 *>(cosT + p * hd + t);
                 sv[k] = *reinterpret_cast<const f32x4 *>(sinT + p * hd + t);
+            }
+            if constexpr (ROPE && GEN) {                           // a chunk may straddle the halves: per element
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int e = 4 * c + q, t = e < half ? e : e - half;
+                    cv[k][q] = cosT[p * hd + t];
+                    sv[k][q] = sinT[p * hd + t];
+                }
             }
         }
     }
@@ -73,7 +82,31 @@ __global__ void __launch_bounds__(256) norm_rope_store_kernel(const float *X, co
             y[k][q] = W ? __fmul_rn(t, wv[k][q]) : t;
         }
     f32x4 o[NV];
-    if constexpr (ROPE) {
+    if constexpr (ROPE && GEN) {
+        // partners through this wave's slice of the row buffer (hd floats per wave)
+        __shared__ float ys[4][1024];
+        float *yw = ys[threadIdx.x >> 6];
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int c = lane + 64 * k;
+            if (c < n4) *reinterpret_cast<f32x4 *>(yw + 4 * c) = y[k];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");          // the wave's row is in LDS before any lane
+        __builtin_amdgcn_wave_barrier();                             // reads its partner (no workgroup barrier:
+                                                                     // waves past the last row have returned)
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int c = lane + 64 * k;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int e = 4 * c + q;
+                const bool lo = e < half;
+                const float pr = c < n4 ? yw[lo ? e + half : e - half] : 0.f;
+                o[k][q] = lo ? __fsub_rn(__fmul_rn(y[k][q], cv[k][q]), __fmul_rn(pr, sv[k][q]))
+                             : __fadd_rn(__fmul_rn(y[k][q], cv[k][q]), __fmul_rn(pr, sv[k][q]));
+            }
+        }
+    } else if constexpr (ROPE) {
 #pragma unroll
         for (int k = 0; k < NV; k++) {
             f32x4 pr;                                                  // the partner chunk's values
@@ -111,17 +144,30 @@ __global__ void __launch_bounds__(256) norm_rope_store_kernel(const float *X, co
 }
 
 bool norm_rope_shape_ok(int hd, bool rope) {
-    if (hd <= 0 || hd % 4 || hd > 1024) return false;
-    if (!rope) return true;
-    // rotate-half partners: same lane (hd a multiple of 512) or a lane XOR (hd a power of two up to 256)
-    return hd == 512 || hd == 1024 || (hd >= 8 && hd <= 256 && (hd & (hd - 1)) == 0);
+    (void)rope;                                      // every hd below has a rotate-half partner layout
+    return hd > 0 && hd % 4 == 0 && hd <= 1024;
 }
+
+// Rotate-half partners in registers: the same lane (hd 512, 1024) or a lane XOR (power-of-two hd up to 256).
+static bool rope_in_registers(int hd) { return hd == 512 || hd == 1024 || (hd >= 8 && hd <= 256 && (hd & (hd - 1)) == 0); }
 
 template <int DT, bool ROPE>
 static hipError_t launch_nrs_t(const float *X, const float *W, void *Y, int rows, int NH, int hd, float eps,
                                const float *cosT, const float *sinT, int base, int pos_step, const int *pos_arr,
                                long slot_stride, long row_stride, hipStream_t st) {
     const dim3 grid((unsigned)((rows + 3) / 4));
+    if (ROPE && !rope_in_registers(hd)) {
+        if (hd <= 256)
+            hipLaunchKernelGGL((norm_rope_store_kernel<DT, ROPE, 1, true>), grid, dim3(256), 0, st, X, W, Y, rows, NH, hd,
+                               eps, cosT, sinT, base, pos_step, pos_arr, slot_stride, row_stride);
+        else if (hd <= 512)
+            hipLaunchKernelGGL((norm_rope_store_kernel<DT, ROPE, 2, true>), grid, dim3(256), 0, st, X, W, Y, rows, NH, hd,
+                               eps, cosT, sinT, base, pos_step, pos_arr, slot_stride, row_stride);
+        else
+            hipLaunchKernelGGL((norm_rope_store_kernel<DT, ROPE, 4, true>), grid, dim3(256), 0, st, X, W, Y, rows, NH, hd,
+                               eps, cosT, sinT, base, pos_step, pos_arr, slot_stride, row_stride);
+        return hipGetLastError();
+    }
     if (hd <= 256)
         hipLaunchKernelGGL((norm_rope_store_kernel<DT, ROPE, 1>), grid, dim3(256), 0, st, X, W, Y, rows, NH, hd, eps, cosT,
                            sinT, base, pos_step, pos_arr, slot_stride, row_stride);

@@ -119,7 +119,7 @@ hipError_t dgx_kv_append(const float *k_src, const float *v_src, void *Kc, void 
  * y = x * rsqrt(mean(x^2) + eps) * W (W == NULL: no scale); with rope != 0 the rotate-half RoPE of position
  * p = pos_arr ? pos_arr[s] : base + s * pos_step from the tables cosT / sinT (row p: entries [p*hd, p*hd + hd/2));
  * stored at Y + s*slot_stride + p*row_stride + h*hd elements of y_dtype (0 fp32, 1 f16, 2 bf16; nearest-even).
- * hd % 4 == 0, hd <= 1024; with rope a power of two up to 256, or 512 / 1024. pos_arr is a device array or null.
+ * hd % 4 == 0, hd <= 1024, with or without rope. pos_arr is a device array or null.
  * Replaces launch_norm_rope_store<TO>() / norm_rope_store_kernel, kernels/norm_fused.cuh:84-133 (the Gemma4 q, k
  * and v appends of models/gemma4_decode.cu:340,353-354 and models/gemma4_batch.cu:142,153,477,486). */
 hipError_t dgx_norm_rope_store(const float *X, const float *W, void *Y, int y_dtype, int rows, int NH, int hd, float eps,

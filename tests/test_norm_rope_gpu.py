@@ -121,11 +121,35 @@ def test_ragged_batch_layout(hd, nkv):
     assert (k[~written] == 0).all(), "rows other than the slots' positions changed"
 
 
+@pytest.mark.parametrize("hd", [96, 100, 384, 768])
+def test_head_dims_with_partners_through_lds(hd):
+    """Head dims whose rotate-half partner is neither in the lane nor one lane swap away (any hd % 4 == 0, as the
+    reference kernel takes them; at hd 100 a 4-element chunk straddles the halves): q rows in fp32 and k rows
+    into a bf16 cache against the oracle."""
+    NQ, S, base, L = 4, 3, 50, 64
+    x, w, cosT, sinT = _inputs(61 + hd, S * NQ, hd, L)
+    Y = torch.empty(S * NQ * hd, device="cuda")
+    A.norm_rope_store(dev(x), dev(w), Y, 0, S * NQ, NQ, hd, EPS, dev(cosT), dev(sinT), base=base, pos_step=1,
+                      slot_stride=NQ * hd, row_stride=0, rope=True)
+    Kc = torch.zeros(L * NQ * hd, device="cuda", dtype=torch.bfloat16)
+    A.norm_rope_store(dev(x), dev(w), Kc, 2, S * NQ, NQ, hd, EPS, dev(cosT), dev(sinT), base=base, pos_step=1,
+                      slot_stride=0, row_stride=NQ * hd, rope=True)
+    torch.cuda.synchronize()
+    ref = oracle.norm_rope_rows(x, w, EPS, cosT, sinT, base + np.arange(S * NQ) // NQ, rope=True)
+    _check(Y.cpu().numpy().reshape(S * NQ, hd), ref, 0, f"q hd={hd}")
+    k = Kc.float().cpu().numpy().reshape(L, NQ * hd)
+    _check(k[base:base + S].reshape(S * NQ, hd), ref, 2, f"k hd={hd}")
+    assert (k[:base] == 0).all() and (k[base + S:] == 0).all()
+
+
 def test_rejects_unsupported_shapes():
-    X = torch.zeros(4 * 96, device="cuda")
-    Y = torch.zeros(4 * 96, device="cuda")
-    with pytest.raises(A.HipError):                                     # rotate-half needs a paired lane layout
-        A.norm_rope_store(X, None, Y, 0, 4, 4, 96, EPS, X, X, rope=True)
+    X = torch.zeros(4 * 98, device="cuda")
+    Y = torch.zeros(4 * 98, device="cuda")
+    for rope in (True, False):                                          # whole 16-byte chunks: hd % 4 == 0
+        with pytest.raises(A.HipError):
+            A.norm_rope_store(X, None, Y, 0, 4, 4, 98, EPS, X, X, rope=rope)
+    with pytest.raises(A.HipError):                                     # beyond the 1024-wide row buffer
+        A.norm_rope_store(X, None, Y, 0, 1, 1, 1028, EPS, X, X, rope=True)
     A.norm_rope_store(X, None, Y, 0, 4, 4, 96, EPS, rope=False)         # plain norm: any hd % 4 == 0
     torch.cuda.synchronize()
 
