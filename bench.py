@@ -288,7 +288,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "tree", "global", "norm", "all"], default="all")
+    ap.add_argument("--only", choices=["decode", "prefill", "tree", "global", "norm", "sliding", "all"], default="all")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB device copy (scale reference for HBM byte counters)")
     args = ap.parse_args()
@@ -310,6 +310,12 @@ def main():
         print(json.dumps({"metric": "norm+RoPE+store GB/s (1024 tokens x 8 kv heads, hd 256, bf16 cache)",
                           "value": round(nby / (nms * 1e-3) / 1e9, 1), "unit": "GB/s", "us_per_call": round(nms * 1e3, 2),
                           "bytes": nby, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True}))
+        return
+    if args.only == "sliding":                # the sliding-window decode alone (profiling); not the headline line
+        sms, sby = run_sliding_decode(args.steps, args.warmup)
+        print(json.dumps({"metric": "sliding-window decode GB/s (B8 ragged <=32K, 1K window, hd 256, bf16)",
+                          "value": round(sby / (sms * 1e-3) / 1e9, 1), "unit": "GB/s", "us_per_call": round(sms * 1e3, 2),
+                          "bytes": sby, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True}))
         return
     if args.only == "tree":                   # the tree-verify workload alone (profiling); not the headline line
         tms, tby = run_tree(args.steps, args.warmup)
