@@ -89,3 +89,49 @@ def test_prefill_graph_replays_with_new_queries():
         A.attn_prefill(Q, K, V, Oe, 1, T, NQ, NKV, HD)
         torch.cuda.synchronize()
         assert torch.equal(Og.view(torch.int16), Oe.view(torch.int16)), f"replay {step}"
+
+
+def test_norm_rope_store_then_decode_graph_replays():
+    """The Gemma decode step's producer and consumer in one captured graph (models/gemma4_decode.cu:340-354 then the
+    split decode): k rows normed, rotated and stored into a bf16 cache at per-slot positions (pos_arr), then the
+    batch decode over that cache. Positions are rewritten in place between replays; every replay equals the eager
+    pair bit for bit (cache and output)."""
+    B, NQ, NKV, HD, ML = 4, 16, 8, 256, 1024
+    g0 = torch.Generator(device="cuda").manual_seed(11)
+    Kc = (torch.randn(B * ML * NKV * HD, device="cuda", generator=g0) * 0.5).bfloat16()
+    Vc = (torch.randn(B * ML * NKV * HD, device="cuda", generator=g0) * 0.5).bfloat16()
+    Kce, Vce = Kc.clone(), Vc.clone()
+    xk = torch.randn(B * NKV * HD, device="cuda", generator=g0)
+    xv = torch.randn(B * NKV * HD, device="cuda", generator=g0)
+    w = torch.randn(HD, device="cuda", generator=g0)
+    cosT, sinT = oracle.rope_tables(ML, HD)
+    C, S = torch.from_numpy(cosT).cuda(), torch.from_numpy(sinT).cuda()
+    Q = torch.randn(B * NQ * HD, device="cuda", generator=g0).bfloat16()
+    pos = torch.full((B,), 10, dtype=torch.int32, device="cuda")
+    stride = ML * NKV * HD
+    Og = torch.empty_like(Q); Oe = torch.empty_like(Q)
+    A.split_reserve(B, NQ, ML, HD)
+
+    def layer(Kt, Vt, O):
+        A.norm_rope_store(xk, w, Kt, 2, B * NKV, NKV, HD, 1e-6, C, S, pos_arr=pos, slot_stride=stride,
+                          row_stride=NKV * HD, rope=True)
+        A.norm_rope_store(xv, None, Vt, 2, B * NKV, NKV, HD, 1e-6, pos_arr=pos, slot_stride=stride,
+                          row_stride=NKV * HD, rope=False)
+        A.attn_batch(Q, Kt, Vt, O, B, 1, NQ, NKV, HD, pos, stride, ML - 1)
+
+    layer(Kc, Vc, Og)                                                    # eager first call (warm-up), on both
+    layer(Kce, Vce, Oe)                                                  # caches so they stay alike
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        layer(Kc, Vc, Og)
+    rng = np.random.default_rng(12)
+    for step in range(4):
+        p = rng.integers(0, ML, size=B).astype(np.int32)
+        pos.copy_(torch.from_numpy(p).cuda())
+        graph.replay()
+        layer(Kce, Vce, Oe)
+        torch.cuda.synchronize()
+        assert torch.equal(Kc.view(torch.int16), Kce.view(torch.int16)), f"replay {step} cache positions {p.tolist()}"
+        assert torch.equal(Vc.view(torch.int16), Vce.view(torch.int16)), f"replay {step} v cache"
+        assert torch.equal(Og.view(torch.int16), Oe.view(torch.int16)), f"replay {step} output"
