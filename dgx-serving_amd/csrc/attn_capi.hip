@@ -408,6 +408,10 @@ hipError_t dgx_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int
     if (!valid_dtype(kv_dtype)) return hipErrorInvalidValue;
     return launch_kv_store(src, dst, n, kv_dtype, which, knob_on("G4_KV_STATS") ? 1 : 0, st);
 }
+hipError_t dgx_f32_to_bf16(const float *in, void *out, size_t n, hipStream_t st) {
+    if (n && (!in || !out)) return hipErrorInvalidValue;
+    return launch_kv_store(in, out, n, DT_BF16, 0, 0, st);        // the store's RN-even conversion, no statistics
+}
 hipError_t dgx_kv_stats(unsigned out[4]) { return read_kv_stats(out); }
 
 hipError_t dgx_norm_rope_store(const float *X, const float *W, void *Y, int y_dtype, int rows, int NH, int hd, float eps,

@@ -41,6 +41,7 @@ def lib():
             "dgx_attn_decode": ([P, P, P, P, I, I, I, I, I, P, F, I], I),
             "dgx_attn_decode_batch": ([P, P, P, P, I, I, I, I, I, L64, P, F, I, P], I),
             "dgx_kv_store": ([P, P, S, I, I, P], I),
+            "dgx_f32_to_bf16": ([P, P, S, P], I),
             "dgx_kv_stats": ([P], I),
             "dgx_kv_append": ([P, P, P, P, I, I, I, L64, I, P, I, P], I),
             "dgx_norm_rope_store": ([P, P, P, I, I, I, I, F, P, P, I, I, P, L64, L64, I, P], I),
@@ -137,6 +138,11 @@ def attn_decode_batch(Q, K, V, O, B, NQ, NKV, HD, base, kv_stride, scale=0.0, wi
 
 def kv_store(src, dst, n, kv_dtype, which):
     _ck(lib().dgx_kv_store(_ptr(src), _ptr(dst), n, kv_dtype, which, _stream()), "dgx_kv_store")
+
+
+def f32_to_bf16(src, dst, n):
+    """launch_f32_to_bf16 (kernels/elementwise.cuh:85-95): RN-even fp32 -> bf16 of n elements."""
+    _ck(lib().dgx_f32_to_bf16(_ptr(src), _ptr(dst), n, _stream()), "dgx_f32_to_bf16")
 
 
 def kv_append(k_src, v_src, Kc, Vc, kv_dtype, nseq, T, kv_stride, row_elems, pos_b=None, base=0):

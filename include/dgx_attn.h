@@ -105,6 +105,9 @@ hipError_t dgx_attn_decode_batch(const float *Q, const float *Kc, const float *V
 /* fp32 -> cache dtype store (RN-even), which = 0 for K, 1 for V; counts non-finite / max |x| with G4_KV_STATS=1.
  * dst already offset by the caller (kv_at). Replaces kv_store() / kv_store_kernel, kernels/kv_store.cuh:76-113. */
 hipError_t dgx_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int which, hipStream_t st);
+/* fp32 -> bf16 (RN-even) of n elements, the Qwen KV-cache hand-off: replaces launch_f32_to_bf16() /
+ * f32_to_bf16_kernel, kernels/elementwise.cuh:85-95 (used per slot at models/qwen35_batch.cu:159-162). */
+hipError_t dgx_f32_to_bf16(const float *in, void *out, size_t n, hipStream_t st);
 /* Read the G4_KV_STATS counters {nonfinite K, nonfinite V, max|K| bits, max|V| bits} (kv_store.cuh:86-98). */
 hipError_t dgx_kv_stats(unsigned out[4]);
 /* Ragged KV append in one launch: token t of sequence b (rows b*T + t of k_src / v_src, fp32 [nseq*T][row_elems])

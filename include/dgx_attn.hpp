@@ -50,6 +50,11 @@ static inline void kv_store(const float *src, float *dst, size_t n, int which, h
     dgx_detail::check(dgx_kv_store(src, dst, n, g4_kv_dtype(), which, st), "kv_store");
 }
 
+// ---- kernels/elementwise.cuh:85-95 (the Qwen KV-cache hand-off)
+static inline void launch_f32_to_bf16(const float *in, __hip_bfloat16 *out, size_t n, hipStream_t s = 0) {
+    dgx_detail::check(dgx_f32_to_bf16(in, out, n, s), "f32_to_bf16");
+}
+
 // One-launch ragged append of B slots x T tokens (replaces the per-slot kv_store loops of models/gemma4_batch.cu:
 // 160-171 and models/qwen35_batch.cu:159-162); pos_b: device array of per-slot positions, or null for `base`.
 static inline void kv_append(const float *k, const float *v, float *Kc, float *Vc, int B, int T, long kv_stride,

@@ -127,6 +127,7 @@ int main() {
         launch_norm_rope_store<__hip_bfloat16>(q, q, const_cast<__hip_bfloat16 *>(kb), 8, 8, 256, 1e-6f, q, q, 100, 1,
                                                nullptr, 0, 8L * 256, true);
         launch_norm_rope_store<float>(q, nullptr, o, 8, 8, 256, 1e-6f, q, q, 100, 1, nullptr, 0, 8L * 256, false);
+        launch_f32_to_bf16(q, const_cast<__hip_bfloat16 *>(kb), 4096);
     }
     float *cache = reinterpret_cast<float *>(0x1000);
     printf("%d %d %d %zu %td\n", g4_kv_dtype(), attn_split_chunk(), attn_split_ns_cap(8192), g4_kv_elem(),

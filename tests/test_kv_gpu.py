@@ -100,3 +100,22 @@ def test_kv_append_uniform_base_and_empty():
     assert np.array_equal(_raw(Vc), _raw(Kc))
     with pytest.raises(A.HipError):
         A.kv_append(kd, kd, Kc, Vc, 2, B, T, ML * row + 2, row, None, 0)  # stride not a multiple of 4
+
+
+@pytest.mark.parametrize("n", [0, 1, 7, 4099])
+def test_f32_to_bf16_matches_the_oracle_rounding(n):
+    """launch_f32_to_bf16 (kernels/elementwise.cuh:85-95): RN-even fp32 -> bf16, bit for bit against the oracle's
+    rounding, including ties, signed zeros, subnormals, infinities and overflow; nothing past n is written."""
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 10).astype(np.float32)
+    special = np.array([0.0, -0.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, 1e-40, -1e-40, np.inf, -np.inf, 3.4e38],
+                       np.float32)
+    x[:min(n, len(special))] = special[:min(n, len(special))]
+    src = torch.from_numpy(x).cuda()
+    dst = torch.full((n + 8,), 0x1234, dtype=torch.int16, device="cuda")
+    A.f32_to_bf16(src, dst, n)
+    torch.cuda.synchronize()
+    out = dst.cpu().numpy().view(np.uint16)
+    _, bits = oracle.round_bf16(x)
+    assert np.array_equal(out[:n], bits)
+    assert (out[n:] == 0x1234).all()
