@@ -230,6 +230,7 @@ bool f32_take_fast(const Problem &p, const Pool *&pool) {
 
 extern "C" {
 
+int dgx_kv_stats_enabled(void) { return knob_on("G4_KV_STATS") ? 1 : 0; }
 int dgx_kv_dtype(void) {
     if (g_kv_override >= 0) return g_kv_override;
     static const int dt = parse_kv_dtype();

@@ -42,6 +42,7 @@ def lib():
             "dgx_attn_decode_batch": ([P, P, P, P, I, I, I, I, I, L64, P, F, I, P], I),
             "dgx_kv_store": ([P, P, S, I, I, P], I),
             "dgx_f32_to_bf16": ([P, P, S, P], I),
+            "dgx_kv_stats_enabled": ([], I),
             "dgx_kv_stats": ([P], I),
             "dgx_kv_append": ([P, P, P, P, I, I, I, L64, I, P, I, P], I),
             "dgx_norm_rope_store": ([P, P, P, I, I, I, I, F, P, P, I, I, P, L64, L64, I, P], I),
@@ -156,6 +157,11 @@ def norm_rope_store(X, W, Y, y_dtype, rows, NH, hd, eps, cosT=None, sinT=None, b
     _ck(lib().dgx_norm_rope_store(_ptr(X), _ptr(W), _ptr(Y), y_dtype, rows, NH, hd, float(eps), _ptr(cosT), _ptr(sinT),
                                   base, pos_step, _ptr(pos_arr), slot_stride, row_stride, 1 if rope else 0, _stream()),
         "dgx_norm_rope_store")
+
+
+def kv_stats_enabled():
+    """g4_kv_stats_enabled() (kernels/kv_store.cuh:87-90): whether G4_KV_STATS=1."""
+    return bool(lib().dgx_kv_stats_enabled())
 
 
 def kv_stats():

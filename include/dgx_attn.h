@@ -37,6 +37,9 @@ extern "C" {
  * G4_ATTN_SPLIT=0). Returns -1 for an invalid value (the C++ wrapper exits 1 like the reference).
  * Replaces g4_kv_dtype(), kernels/kv_store.cuh:23-35. */
 int dgx_kv_dtype(void);
+/* 1 when G4_KV_STATS=1 (the stores count non-finite values and max |x|), else 0. Replaces the knob test of
+ * g4_kv_stats_enabled(), kernels/kv_store.cuh:87-90. */
+int dgx_kv_stats_enabled(void);
 /* Force fp32 KV for this process (MoE models). Replaces g4_kv_force_fp32(), kernels/kv_store.cuh:37-41. */
 void dgx_kv_force_fp32(const char *why);
 /* Bytes per stored KV element (4 or 2). Replaces g4_kv_elem(), kernels/kv_store.cuh:42. */

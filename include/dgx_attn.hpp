@@ -10,6 +10,7 @@
 #include <cstddef>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <type_traits>
 #include <hip/hip_runtime_api.h>
 #include <hip/hip_fp16.h>
@@ -40,6 +41,23 @@ inline int g4_kv_dtype() {
     return d;
 }
 inline void g4_kv_force_fp32(const char *why) { dgx_kv_force_fp32(why); }
+// kernels/kv_store.cuh:87-99: G4_KV_STATS=1 turns the store statistics on; they are reported once at exit.
+static inline bool g4_kv_stats_enabled() {
+    static const bool on = []() {
+        if (!dgx_kv_stats_enabled()) return false;
+        atexit([]() {
+            unsigned h[4] = {0, 0, 0, 0};
+            if (dgx_kv_stats(h) == hipSuccess) {
+                float mk, mv;
+                memcpy(&mk, &h[2], 4); memcpy(&mv, &h[3], 4);
+                fprintf(stderr, "G4_KV_STATS dtype=%d nonfinite_k=%u nonfinite_v=%u max_abs_k=%.9g max_abs_v=%.9g\n",
+                        dgx_kv_dtype(), h[0], h[1], mk, mv);
+            }
+        });
+        return true;
+    }();
+    return on;
+}
 static inline size_t g4_kv_elem() { return g4_kv_dtype() == KV_FP32 ? 4 : 2; }
 // Byte-offset arithmetic on float* cache handles whatever the storage dtype (kv_store.cuh:47-50).
 template <class P> static inline P *kv_at(P *p, size_t elems) {
@@ -72,6 +90,15 @@ static inline void launch_norm_rope_store(const float *X, const float *W, TO *Y,
     dgx_detail::check(dgx_norm_rope_store(X, W, Y, dgx_detail::kv_code<TO>(), rows, NH, hd, eps, cosT, sinT, base,
                                           pos_step, pos_arr, slot_stride, row_stride, rope ? 1 : 0, s),
                       "norm_rope_store");
+}
+
+// ---- kernels/attention.cuh:13-22. The reference aborts when attn_decode_kernel's per-row score buffer (context +
+// head dim floats of shared memory) exceeds the device's opt-in limit. No kernel here keeps a score row in LDS (every
+// decode path streams its keys through an online softmax), so every context length runs and the guard has nothing
+// to reject; attn_decode_kernel names the guarded kernel only so that callers compile unchanged.
+static const char attn_decode_kernel[1] = {0};
+static inline void attn_smem_guard(const void *kernel, size_t shmem, const char *who, int ctxlen) {
+    (void)kernel; (void)shmem; (void)who; (void)ctxlen;
 }
 
 // ---- kernels/attention.cuh:72-198 (fp32 caches)

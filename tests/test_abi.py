@@ -45,7 +45,8 @@ def _knobs(env):
     code = textwrap.dedent(f"""
         import ctypes
         L = ctypes.CDLL({LIB!r})
-        print(L.dgx_kv_dtype(), L.dgx_attn_split_chunk(), L.dgx_attn_split_ns_cap(1000), L.dgx_kv_elem())
+        print(L.dgx_kv_dtype(), L.dgx_attn_split_chunk(), L.dgx_attn_split_ns_cap(1000), L.dgx_kv_elem(),
+              L.dgx_kv_stats_enabled())
     """)
     e = {k: v for k, v in os.environ.items() if not k.startswith(("G4_", "DGX_KNOBS"))}
     e.update(env)
@@ -55,10 +56,11 @@ def _knobs(env):
 
 
 def test_kv_dtype_and_chunk_knobs(tmp_path):
-    assert _knobs({})[0] == [1, 256, 4, 2]                         # unset -> f16; MI355X chunk default 256
+    assert _knobs({})[0] == [1, 256, 4, 2, 0]                      # unset -> f16; MI355X chunk default 256
+    assert _knobs({"G4_KV_STATS": "1"})[0][4] == 1                  # g4_kv_stats_enabled (kv_store.cuh:87-90)
     assert _knobs({"G4_ATTN_SPLIT": "0"})[0][0] == 0                # split off -> fp32 KV (kv_store.cuh:29-31)
     assert _knobs({"G4_KV_DTYPE": "bf16"})[0][0] == 2
-    assert _knobs({"G4_KV_DTYPE": "fp32"})[0] == [0, 256, 4, 4]
+    assert _knobs({"G4_KV_DTYPE": "fp32"})[0][:4] == [0, 256, 4, 4]
     v, err = _knobs({"G4_KV_DTYPE": "fp8"})
     assert v[0] == -1 and "Invalid G4_KV_DTYPE" in err
     assert _knobs({"G4_ATTN_CHUNK": "64"})[0][1:3] == [64, 16]
@@ -128,6 +130,8 @@ int main() {
                                                nullptr, 0, 8L * 256, true);
         launch_norm_rope_store<float>(q, nullptr, o, 8, 8, 256, 1e-6f, q, q, 100, 1, nullptr, 0, 8L * 256, false);
         launch_f32_to_bf16(q, const_cast<__hip_bfloat16 *>(kb), 4096);
+        if (g4_kv_stats_enabled()) printf("stats on\n");
+        attn_smem_guard((const void *)attn_decode_kernel, (size_t)(256 + 4096) * sizeof(float), "attn_decode", 4096);
     }
     float *cache = reinterpret_cast<float *>(0x1000);
     printf("%d %d %d %zu %td\n", g4_kv_dtype(), attn_split_chunk(), attn_split_ns_cap(8192), g4_kv_elem(),
