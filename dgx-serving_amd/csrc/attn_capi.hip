@@ -230,6 +230,10 @@ bool f32_take_fast(const Problem &p, const Pool *&pool) {
 
 extern "C" {
 
+size_t dgx_flash_attn_hd512_lds(void) {
+    const size_t a = split_lds_bytes(512), b = prefill_lds_bytes(512);
+    return a > b ? a : b;
+}
 int dgx_kv_stats_enabled(void) { return knob_on("G4_KV_STATS") ? 1 : 0; }
 int dgx_kv_dtype(void) {
     if (g_kv_override >= 0) return g_kv_override;

@@ -80,6 +80,8 @@ hipError_t launch_decode_f32(const Problem &p, int chunk, const Partials &part, 
 hipError_t launch_prefill(const Problem &p, int kv_split, const Partials &part, hipStream_t st);
 // The key split chosen for kv_split = -1 (0: none).
 int prefill_auto_split(const Problem &p);
+size_t prefill_lds_bytes(int HD);   // dynamic LDS of the HD-wide prefill tile (W = 0)
+size_t split_lds_bytes(int HD);     // dynamic LDS of split_kernel at one row block
 // LSE combine of split partials for every (row, head).
 hipError_t launch_combine(const Problem &p, int chunk, const Partials &part, hipStream_t st);
 // Scratch requirement (rows*NQ*ns_cap) of a problem at a given chunk.

@@ -650,6 +650,15 @@ static int pref_per_cu(int HD) { return pref_shape(HD, 0).per_cu; }
 
 // Key split for kv_split = -1: when the unsplit grid would fill at most half of the workgroup slots (a short run
 // of queries over a long cached prefix), cut the keys into as many absolute splits as whole grids fit on them.
+size_t prefill_lds_bytes(int HD) {
+    switch (HD) {
+    case 128: return PrefTileCfg<128, 0>::LDS;
+    case 256: return PrefTileCfg<256, 0>::LDS;
+    case 512: return PrefTileCfg<512, 0>::LDS;
+    default: return 0;
+    }
+}
+
 int prefill_auto_split(const Problem &p) {
     if (p.NQ % p.NKV) return 0;
     const int GRP = p.NQ / p.NKV, HR = pref_half_rows(p.HD);

@@ -924,6 +924,15 @@ hipError_t launch_split(const Problem &p, int chunk, Partials &part, hipStream_t
     return e;
 }
 
+size_t split_lds_bytes(int HD) {
+    switch (HD) {
+    case 128: return SplitCfg<128, 1>::LDS;
+    case 256: return SplitCfg<256, 1>::LDS;
+    case 512: return SplitCfg<512, 1>::LDS;
+    default: return 0;
+    }
+}
+
 hipError_t launch_combine(const Problem &p, int chunk, const Partials &part, hipStream_t st) {
     const int rows = p.nseq * p.T * p.NQ;
     if (rows <= 0) return hipSuccess;

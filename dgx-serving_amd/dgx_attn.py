@@ -43,6 +43,7 @@ def lib():
             "dgx_kv_store": ([P, P, S, I, I, P], I),
             "dgx_f32_to_bf16": ([P, P, S, P], I),
             "dgx_kv_stats_enabled": ([], I),
+            "dgx_flash_attn_hd512_lds": ([], S),
             "dgx_kv_stats": ([P], I),
             "dgx_kv_append": ([P, P, P, P, I, I, I, L64, I, P, I, P], I),
             "dgx_norm_rope_store": ([P, P, P, I, I, I, I, F, P, P, I, I, P, L64, L64, I, P], I),
@@ -157,6 +158,11 @@ def norm_rope_store(X, W, Y, y_dtype, rows, NH, hd, eps, cosT=None, sinT=None, b
     _ck(lib().dgx_norm_rope_store(_ptr(X), _ptr(W), _ptr(Y), y_dtype, rows, NH, hd, float(eps), _ptr(cosT), _ptr(sinT),
                                   base, pos_step, _ptr(pos_arr), slot_stride, row_stride, 1 if rope else 0, _stream()),
         "dgx_norm_rope_store")
+
+
+def flash_attn_hd512_lds():
+    """configure_flash_attn_hd512() (kernels/attention_flash.cuh:254-270): LDS bytes of the HD 512 flash path."""
+    return int(lib().dgx_flash_attn_hd512_lds())
 
 
 def kv_stats_enabled():

@@ -37,6 +37,10 @@ extern "C" {
  * G4_ATTN_SPLIT=0). Returns -1 for an invalid value (the C++ wrapper exits 1 like the reference).
  * Replaces g4_kv_dtype(), kernels/kv_store.cuh:23-35. */
 int dgx_kv_dtype(void);
+/* Dynamic LDS bytes of the head-dim 512 flash path (the larger of its short-query split and prefill tiles; each
+ * kernel sets its own limit at its first launch, within the 160 KB of a gfx950 CU). Replaces the value that
+ * configure_flash_attn_hd512() returns, kernels/attention_flash.cuh:254-270. */
+size_t dgx_flash_attn_hd512_lds(void);
 /* 1 when G4_KV_STATS=1 (the stores count non-finite values and max |x|), else 0. Replaces the knob test of
  * g4_kv_stats_enabled(), kernels/kv_store.cuh:87-90. */
 int dgx_kv_stats_enabled(void);

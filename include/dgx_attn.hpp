@@ -141,6 +141,13 @@ static inline void launch_attn_decode_split(const float *Q, const float *Kc, con
 static inline void reserve_flash_attn_scratch(size_t need, size_t hd) {
     dgx_detail::check(dgx_flash_attn_reserve_partials(need, (int)hd), "flash_attn reserve");
 }
+// The reference raises the HD 512 kernel's shared-memory opt-in here and returns its size; the gfx950 kernels set
+// their LDS limit at first launch, so this only reports the bytes (tile shape and waves are the library's).
+template <int BC, int NW, typename KV>
+static inline size_t configure_flash_attn_hd512() {
+    (void)dgx_detail::kv_code<KV>();
+    return dgx_flash_attn_hd512_lds();
+}
 template <int HD, int BC, int NW, typename KV>
 static inline void launch_flash_attn2bs(const float *Q, const KV *Kc, const KV *Vc, float *O, int Sq, int NQ, int NKV,
                                         int base, hipStream_t st = 0, const unsigned *anc = nullptr,
