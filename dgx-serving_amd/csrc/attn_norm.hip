@@ -6,7 +6,7 @@
 //
 // Row r = (token s = r / NH, head h = r % NH) of hd fp32 values. One wave64 per row, four rows per workgroup:
 // lane l holds the float4 chunks l, l + 64, ... of the row (hd / 4 chunks), so the whole row lives in registers
-// and nothing goes through LDS.
+// (LDS holds a row only for the rotation partners of head dims whose partner is not in a register, see RoPE).
 //   * RMS: each lane sums the squares of its chunks in order, the wave adds the 64 lane sums with a fixed
 //     butterfly; the order depends only on hd, so a row's bits do not depend on how many rows share the launch.
 //     inv = rsqrt(ss / hd + eps); y = (x * inv) * W (two roundings, as the reference's norm_par_mul).
