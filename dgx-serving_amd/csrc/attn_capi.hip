@@ -413,6 +413,10 @@ hipError_t dgx_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int
     if (!valid_dtype(kv_dtype)) return hipErrorInvalidValue;
     return launch_kv_store(src, dst, n, kv_dtype, which, knob_on("G4_KV_STATS") ? 1 : 0, st);
 }
+hipError_t dgx_gate_sigmoid(float *y, const float *gate, int n, hipStream_t st) {
+    if (n < 0 || (n && (!y || !gate))) return hipErrorInvalidValue;
+    return launch_gate_sigmoid(y, gate, (size_t)n, st);
+}
 hipError_t dgx_f32_to_bf16(const float *in, void *out, size_t n, hipStream_t st) {
     if (n && (!in || !out)) return hipErrorInvalidValue;
     return launch_kv_store(in, out, n, DT_BF16, 0, 0, st);        // the store's RN-even conversion, no statistics

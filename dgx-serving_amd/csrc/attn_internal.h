@@ -96,6 +96,7 @@ hipError_t launch_scalar_decode(const float *Q, const float *Kc, const float *Vc
 hipError_t launch_scalar_rows(const float *Q, const float *Kc, const float *Vc, float *O, int rows, int NQ, int NKV,
                               int HD, int base, int pos_step, const int *pos_arr, long kv_stride, float scale,
                               int window, int reverse, hipStream_t st);
+hipError_t launch_gate_sigmoid(float *y, const float *gate, size_t n, hipStream_t st);
 hipError_t launch_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int which, int stats,
                            hipStream_t st);
 hipError_t launch_kv_append(const float *ks, const float *vs, void *Kc, void *Vc, int kv_dtype, int nseq, int T,

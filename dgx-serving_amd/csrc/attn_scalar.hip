@@ -149,6 +149,35 @@ __global__ void __launch_bounds__(256) kv_store_kernel(const float *src, uint16_
     }
 }
 
+// y[i] *= sigmoid(gate[i]) in place, fp32, with the factor 1 / (1 + 2^(-g log2 e)) of the fused output gate of the
+// split path (the same float operations, so a separately gated output equals the fused one bit for bit). Four
+// elements per thread with 16-byte accesses when both arrays are 16-byte aligned, else one.
+template <bool VEC>
+__global__ void __launch_bounds__(256) gate_sigmoid_kernel(float *y, const float *gate, size_t n) {
+    const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * (VEC ? 4 : 1);
+    if (i >= n) return;
+    if (VEC && i + 4 <= n) {
+        f32x4 v = *reinterpret_cast<const f32x4 *>(y + i);
+        const f32x4 g = *reinterpret_cast<const f32x4 *>(gate + i);
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] *= 1.f / (1.f + fast_exp2(-g[e] * kLog2e));
+        *reinterpret_cast<f32x4 *>(y + i) = v;
+    } else {
+        for (size_t j = i; j < n && j < i + (VEC ? 4 : 1); j++) y[j] *= 1.f / (1.f + fast_exp2(-gate[j] * kLog2e));
+    }
+}
+
+hipError_t launch_gate_sigmoid(float *y, const float *gate, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    const bool vec = ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(gate)) & 15) == 0;
+    const size_t threads = vec ? (n + 3) / 4 : n;
+    if ((threads + 255) / 256 > 0x7fffffffu) return hipErrorInvalidConfiguration;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (vec) hipLaunchKernelGGL(gate_sigmoid_kernel<true>, grid, dim3(256), 0, st, y, gate, n);
+    else hipLaunchKernelGGL(gate_sigmoid_kernel<false>, grid, dim3(256), 0, st, y, gate, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int which, int stats, hipStream_t st) {
     if (n == 0) return hipSuccess;
     if (which < 0 || which > 1) return hipErrorInvalidValue;

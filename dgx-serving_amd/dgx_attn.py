@@ -42,6 +42,7 @@ def lib():
             "dgx_attn_decode_batch": ([P, P, P, P, I, I, I, I, I, L64, P, F, I, P], I),
             "dgx_kv_store": ([P, P, S, I, I, P], I),
             "dgx_f32_to_bf16": ([P, P, S, P], I),
+            "dgx_gate_sigmoid": ([P, P, I, P], I),
             "dgx_kv_stats_enabled": ([], I),
             "dgx_flash_attn_hd512_lds": ([], S),
             "dgx_kv_stats": ([P], I),
@@ -140,6 +141,11 @@ def attn_decode_batch(Q, K, V, O, B, NQ, NKV, HD, base, kv_stride, scale=0.0, wi
 
 def kv_store(src, dst, n, kv_dtype, which):
     _ck(lib().dgx_kv_store(_ptr(src), _ptr(dst), n, kv_dtype, which, _stream()), "dgx_kv_store")
+
+
+def gate_sigmoid(y, gate, n):
+    """launch_gate_sigmoid (kernels/elementwise.cuh:50-60): y *= sigmoid(gate) in place, fp32."""
+    _ck(lib().dgx_gate_sigmoid(_ptr(y), _ptr(gate), n, _stream()), "dgx_gate_sigmoid")
 
 
 def f32_to_bf16(src, dst, n):

@@ -112,6 +112,11 @@ hipError_t dgx_attn_decode_batch(const float *Q, const float *Kc, const float *V
 /* fp32 -> cache dtype store (RN-even), which = 0 for K, 1 for V; counts non-finite / max |x| with G4_KV_STATS=1.
  * dst already offset by the caller (kv_at). Replaces kv_store() / kv_store_kernel, kernels/kv_store.cuh:76-113. */
 hipError_t dgx_kv_store(const float *src, void *dst, size_t n, int kv_dtype, int which, hipStream_t st);
+/* y[i] *= sigmoid(gate[i]) for n fp32 elements in place, the Qwen3.5 full-attention output gate applied after the
+ * attention call, with the same float operations as the gate fused into dgx_attn_batch_ex. Replaces
+ * launch_gate_sigmoid() / gate_sigmoid_kernel, kernels/elementwise.cuh:50-60 (models/qwen35.cu:96,
+ * models/qwen35_decode.cu:166, models/qwen35_batch.cu:168,336). */
+hipError_t dgx_gate_sigmoid(float *y, const float *gate, int n, hipStream_t st);
 /* fp32 -> bf16 (RN-even) of n elements, the Qwen KV-cache hand-off: replaces launch_f32_to_bf16() /
  * f32_to_bf16_kernel, kernels/elementwise.cuh:85-95 (used per slot at models/qwen35_batch.cu:159-162). */
 hipError_t dgx_f32_to_bf16(const float *in, void *out, size_t n, hipStream_t st);

@@ -68,6 +68,10 @@ static inline void kv_store(const float *src, float *dst, size_t n, int which, h
     dgx_detail::check(dgx_kv_store(src, dst, n, g4_kv_dtype(), which, st), "kv_store");
 }
 
+// ---- kernels/elementwise.cuh:50-60 (the Qwen3.5 output gate after attention)
+static inline void launch_gate_sigmoid(float *y, const float *gate, int n, hipStream_t s = 0) {
+    dgx_detail::check(dgx_gate_sigmoid(y, gate, n, s), "gate_sigmoid");
+}
 // ---- kernels/elementwise.cuh:85-95 (the Qwen KV-cache hand-off)
 static inline void launch_f32_to_bf16(const float *in, __hip_bfloat16 *out, size_t n, hipStream_t s = 0) {
     dgx_detail::check(dgx_f32_to_bf16(in, out, n, s), "f32_to_bf16");

@@ -130,6 +130,7 @@ int main() {
                                                nullptr, 0, 8L * 256, true);
         launch_norm_rope_store<float>(q, nullptr, o, 8, 8, 256, 1e-6f, q, q, 100, 1, nullptr, 0, 8L * 256, false);
         launch_f32_to_bf16(q, const_cast<__hip_bfloat16 *>(kb), 4096);
+        launch_gate_sigmoid(o, q, 4096);
         if (g4_kv_stats_enabled()) printf("stats on\n");
         printf("%zu\n", configure_flash_attn_hd512<16, 8, __hip_bfloat16>());
         attn_smem_guard((const void *)attn_decode_kernel, (size_t)(256 + 4096) * sizeof(float), "attn_decode", 4096);

@@ -89,3 +89,34 @@ def test_batch_ex_validation():
         A.attn_batch_ex(Q, O, 1, 1, 24, 4, 256, None, 10, Kp=ptrs, kv_dtype=1)
     with pytest.raises(A.HipError):                       # neither pointers nor caches
         A.attn_batch_ex(Q, O, 1, 1, 24, 4, 256, None, 10, kv_dtype=1)
+
+
+@pytest.mark.parametrize("n,offset", [(24 * 256 * 4, 0), (1001, 0), (4099, 1)])
+def test_standalone_gate_matches_fused_and_sigmoid(n, offset):
+    """launch_gate_sigmoid after attention (models/qwen35_decode.cu:166): against fp64 y * sigmoid(g) within the fp32
+    rounding bar of the fused gate, on aligned and unaligned arrays with tails; and, on an fp32 attention output, bit
+    for bit equal to the gate fused into dgx_attn_batch_ex."""
+    g0 = torch.Generator(device="cuda").manual_seed(n)
+    yb = torch.randn(n + offset, device="cuda", generator=g0)
+    gb = torch.randn(n + offset, device="cuda", generator=g0) * 4.0
+    y, gate = yb[offset:], gb[offset:]
+    y0 = y.cpu().numpy().astype(np.float64)
+    A.gate_sigmoid(y, gate, n)
+    torch.cuda.synchronize()
+    want = y0 / (1.0 + np.exp(-gate.cpu().numpy().astype(np.float64)))
+    err = np.abs(y.cpu().numpy().astype(np.float64) - want)
+    assert (err <= 4e-6 * np.abs(want) + 1e-7).all(), f"max err {err.max():.3e}"
+    if offset == 0 and n == 24 * 256 * 4:
+        B, Tq, NQ, NKV, HD = 4, 1, 24, 4, 256
+        lens = np.array([700, 1300, 64, 2049], np.int32)
+        _, _, _, _, Kc, Vc, ML = _slots(3, B, lens, NKV, HD, torch.float16)
+        Qf = torch.randn(B * NQ * HD, device="cuda", generator=g0)
+        base_b = torch.from_numpy(lens - 1).cuda()
+        A.split_reserve(B, NQ, int(lens.max()), HD)
+        O = torch.empty(B * NQ * HD, device="cuda"); Og = torch.empty_like(O)
+        A.attn_batch_ex(Qf, O, B, Tq, NQ, NKV, HD, base_b, int(lens.max()) - 1, K=Kc, V=Vc, kv_stride=ML * NKV * HD)
+        A.attn_batch_ex(Qf, Og, B, Tq, NQ, NKV, HD, base_b, int(lens.max()) - 1, K=Kc, V=Vc, kv_stride=ML * NKV * HD,
+                        gate=gate)
+        A.gate_sigmoid(O, gate, B * NQ * HD)
+        torch.cuda.synchronize()
+        assert torch.equal(O.view(torch.int32), Og.view(torch.int32)), "separate gate differs from the fused one"
