@@ -241,7 +241,7 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
         for (int i = 0; i < 4; i++) pv[i] = fast_exp2(tv[i] - m);   // exp2(-inf) = 0; m is finite once a key is seen
         if (m == kNegInf) pv[0] = pv[1] = pv[2] = pv[3] = 0.f;
         l += (pv[0] + pv[1]) + (pv[2] + pv[3]);
-        const u32x2 pop = u32x2{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3])};
+        const PFrag<F16> pop = p_frag<F16>(pv[0], pv[1], pv[2], pv[3]);
         // O^T += V^T P^T (16x16x16): stage the V tile in this wave's LDS slice, read it back transposed.
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -253,7 +253,7 @@ __global__ void __launch_bounds__(NKL_ * RW_ * 64) decode_stream_kernel(const De
         if (more) load_t(k + 1, kr, vr, 2);
         const uint16_t *vt = vs + (4 * g + (ln >> 2)) * Cf::VSTR + 4 * (ln & 3);
 #pragma unroll
-        for (int db = 0; db < Cf::DB; db++) acc[db] = mfma16k16<F16>(lds_read_tr16(vt + 16 * db), pop, acc[db]);
+        for (int db = 0; db < Cf::DB; db++) acc[db] = mfma_pv16<F16>(lds_read_tr16(vt + 16 * db), pop, acc[db]);
     };
     for (int k = k0; k < k1; k++) {
         if (!EARLY) load(k, kb, vb);

@@ -56,6 +56,23 @@ template <bool F16> __device__ __forceinline__ uint32_t pack2(float a, float b) 
     if constexpr (F16) { const f16x2 v = {(_Float16)a, (_Float16)b}; return __builtin_bit_cast(uint32_t, v); }
     else { const bf16x2 v = {(__bf16)a, (__bf16)b}; return __builtin_bit_cast(uint32_t, v); }
 }
+// Probabilities as the B operand of the PV MFMA. An f16 operand carries p to 11 significant bits (relative error
+// <= 2^-12). A bf16 operand would carry 8 (2^-9: 4.5e-3 on an output of magnitude 2.5 from a two-key row), so for
+// bf16 p is split into hi = RN_bf16(p) and lo = RN_bf16(p - hi) (p - hi is exact in fp32), fed to two MFMAs:
+// hi + lo carries p to about 16 bits (relative error <= 2^-17).
+template <bool F16> struct PFrag { u32x2 hi, lo; };
+template <bool F16> __device__ __forceinline__ PFrag<F16> p_frag(float p0, float p1, float p2, float p3) {
+    PFrag<F16> f;
+    f.hi = u32x2{pack2<F16>(p0, p1), pack2<F16>(p2, p3)};
+    if constexpr (!F16) {
+        const float h0 = __uint_as_float(f.hi[0] << 16), h1 = __uint_as_float(f.hi[0] & 0xffff0000u);
+        const float h2 = __uint_as_float(f.hi[1] << 16), h3 = __uint_as_float(f.hi[1] & 0xffff0000u);
+        f.lo = u32x2{pack2<F16>(p0 - h0, p1 - h1), pack2<F16>(p2 - h2, p3 - h3)};
+    } else {
+        f.lo = u32x2{0u, 0u};
+    }
+    return f;
+}
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 template <int DT> __device__ __forceinline__ float elem_to_f32(typename Elem<DT>::T v) {
@@ -141,6 +158,21 @@ __device__ __forceinline__ f32x4 mfma16k16(const u32x2 &a, const u32x2 &b, const
         return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
 }
 
+
+// acc += V^T P^T with the P fragment split as above (hi, then lo for bf16).
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma_pv16(const u32x2 &v, const PFrag<F16> &p, f32x4 c) {
+    c = mfma16k16<F16>(v, p.hi, c);
+    if constexpr (!F16) c = mfma16k16<F16>(v, p.lo, c);
+    return c;
+}
+// The 16x16x32 form over two sub-tiles: B = (P of sub-tile 0, P of sub-tile 1) in k-groups of 4 keys.
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma_pv32(const u32x4 &v, const PFrag<F16> &p0, const PFrag<F16> &p1, f32x4 c) {
+    c = mfma16<F16>(v, u32x4{p0.hi[0], p0.hi[1], p1.hi[0], p1.hi[1]}, c);
+    if constexpr (!F16) c = mfma16<F16>(v, u32x4{p0.lo[0], p0.lo[1], p1.lo[0], p1.lo[1]}, c);
+    return c;
+}
 
 // LDS transpose read (gfx950 ds_read_b64_tr_b16). Within each 16-lane group g, lane i passes the address of
 // row 4g + i/4, columns 4*(i%4)..+3 of a row-major 16-bit tile; lane n of the group receives column n of

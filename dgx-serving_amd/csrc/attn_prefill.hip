@@ -386,17 +386,17 @@ prefill_kernel(const PrefArgs a) {
             }
         }
         while (pt < 3) issue_pt(nxt, pt++);
-        u32x2 pop[NSUB][RB];
+        PFrag<F16> pop[NSUB][RB];
 #pragma unroll
         for (int sub = 0; sub < NSUB; sub++)
 #pragma unroll
             for (int rb = 0; rb < RB; rb++) {
-                if (!((ACT >> rb) & 1)) { pop[sub][rb] = u32x2{0u, 0u}; continue; }
+                if (!((ACT >> rb) & 1)) { pop[sub][rb] = PFrag<F16>{u32x2{0u, 0u}, u32x2{0u, 0u}}; continue; }
                 float pv[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) pv[i] = (tv[sub][rb][i] == kNegInf) ? 0.f : fast_exp2(tv[sub][rb][i] - m[rb]);
                 l[rb] += (pv[0] + pv[1]) + (pv[2] + pv[3]);
-                pop[sub][rb] = u32x2{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3])};
+                pop[sub][rb] = p_frag<F16>(pv[0], pv[1], pv[2], pv[3]);
             }
         if constexpr (NSUB == 2) {
             // PV on 16x16x32 over both sub-tiles at once (the order of keys inside an MFMA's reduction is free):
@@ -414,7 +414,6 @@ prefill_kernel(const PrefArgs a) {
                         asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(dst[2 * j + sub])
                                      : "v"((vbase + sub * 16 * ROWB) ^ (32u * (b * PB + j))) : "memory");
             };
-            const u32x4 pp = u32x4{pop[0][0][0], pop[0][0][1], pop[1][0][0], pop[1][0][1]};
             rdv(0, vb2[0]);
 #pragma unroll
             for (int b = 0; b < NPB; b++) {
@@ -429,8 +428,8 @@ prefill_kernel(const PrefArgs a) {
                 }
 #pragma unroll
                 for (int j = 0; j < PB; j++)
-                    acc[0][b * PB + j] = mfma16<F16>(u32x4{cur[2 * j][0], cur[2 * j][1], cur[2 * j + 1][0], cur[2 * j + 1][1]},
-                                                     pp, acc[0][b * PB + j]);
+                    acc[0][b * PB + j] = mfma_pv32<F16>(u32x4{cur[2 * j][0], cur[2 * j][1], cur[2 * j + 1][0], cur[2 * j + 1][1]},
+                                                        pop[0][0], pop[1][0], acc[0][b * PB + j]);
                 if (pt < NPART && b % 2 == 1) issue_pt(nxt, pt++);
             }
         }
@@ -458,7 +457,7 @@ prefill_kernel(const PrefArgs a) {
                 }
                 const int sub = b / (DB / PB), d0 = (b % (DB / PB)) * PB;
 #pragma unroll
-                for (int j = 0; j < PB; j++) acc[0][d0 + j] = mfma16k16<F16>(cur[j], pop[sub][0], acc[0][d0 + j]);
+                for (int j = 0; j < PB; j++) acc[0][d0 + j] = mfma_pv16<F16>(cur[j], pop[sub][0], acc[0][d0 + j]);
                 if (pt < NPART && b % 2 == 1) issue_pt(nxt, pt++);
             }
         }

@@ -435,7 +435,7 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
         // kRescaleThreshold). l holds this lane's share of the row sum; the four lanes of a row are added once,
         // after the loop.
         const bool full = jt >= j_lo && jt + Cf::KT <= j_hi && jt >= lo_max && jt + Cf::KT - 1 <= pos_min;
-        u32x2 pop[NSUB][RBW];
+        PFrag<F16> pop[NSUB][RBW];
         float tv[NSUB][RBW][4];
         bool need = false;
 #pragma unroll
@@ -479,7 +479,7 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
                 float pv[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) { pv[i] = (tv[sub][rb][i] == kNegInf) ? 0.f : fast_exp2(tv[sub][rb][i] - m[rb]); l[rb] += pv[i]; }
-                pop[sub][rb] = u32x2{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3])};
+                pop[sub][rb] = p_frag<F16>(pv[0], pv[1], pv[2], pv[3]);
             }
         // O^T[this wave's dims] += V^T P^T (16x16x16): the A fragment is a transposed LDS read of the V tile.
 #pragma unroll
@@ -489,7 +489,7 @@ __global__ void __launch_bounds__(256) split_kernel(const SplitArgs a) {
             for (int db = 0; db < DBN; db++) {
                 const u32x2 vop = lds_read_tr16(vtr + 16 * db);
 #pragma unroll
-                for (int rb = 0; rb < RBW; rb++) acc[rb][db] = mfma16k16<F16>(vop, pop[sub][rb], acc[rb][db]);
+                for (int rb = 0; rb < RBW; rb++) acc[rb][db] = mfma_pv16<F16>(vop, pop[sub][rb], acc[rb][db]);
             }
         }
     };
@@ -717,7 +717,7 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
         float pv[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) { pv[i] = (tv[i] == kNegInf) ? 0.f : fast_exp2(tv[i] - m); l += pv[i]; }
-        const u32x2 pop = u32x2{pack2<F16>(pv[0], pv[1]), pack2<F16>(pv[2], pv[3])};
+        const PFrag<F16> pop = p_frag<F16>(pv[0], pv[1], pv[2], pv[3]);
 #pragma unroll
         for (int d8 = 0; d8 < DB; d8 += 8) {
             u32x2 v[8];
@@ -727,7 +727,7 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
             asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]),
                          "+v"(v[5]), "+v"(v[6]), "+v"(v[7])::"memory");
 #pragma unroll
-            for (int j = 0; j < 8; j++) acc[d8 + j] = mfma16k16<F16>(v[j], pop, acc[d8 + j]);
+            for (int j = 0; j < 8; j++) acc[d8 + j] = mfma_pv16<F16>(v[j], pop, acc[d8 + j]);
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");        // no load may land after the workgroup ends
