@@ -102,7 +102,7 @@ def run_prefill(steps, warmup, T=1024, NQ=16, NKV=8, HD=256, base=0, window=0, k
     return ms, flops
 
 
-def run_tree(steps, warmup, seed=5):
+def run_tree(steps, warmup, seed=5, runs=None):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     B, NQ, NKV, HD, Tq = 16, 24, 4, 256, 8
     rng = np.random.default_rng(seed)
@@ -130,8 +130,11 @@ def run_tree(steps, warmup, seed=5):
     max_pos = int(committed.max()) + Tq - 1
     A.split_reserve(B * Tq, NQ, max_pos + 1, HD)
     chunk = int(os.environ.get("BENCH_TREE_CHUNK", "512"))
+    # 0: per-sequence chunks (the library default, batch-invariant), 1: equal runs over the batch
+    prev = A.verify_runs(int(os.environ.get("BENCH_VERIFY_RUNS", "0")) if runs is None else runs)
     fn = lambda: A.attn_batch(Q, K, V, O, B, Tq, NQ, NKV, HD, base_b, ML * NKV * HD, max_pos, chunk=chunk, anc=ancd)
     ms = timed(fn, steps, warmup)
+    A.verify_runs(prev)
     nbytes = int((committed + Tq).sum()) * NKV * HD * 4 + 2 * Q.numel() * 2
     return ms, nbytes
 
@@ -210,19 +213,24 @@ def run_norm_rope(steps, warmup, T=1024, NKV=8, HD=256):
 
 
 def _cpu_model():
+    """The host CPU as /proc/cpuinfo names it, with its family / model / stepping numbers (some hosts report only
+    a generic model name)."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = (x.strip() for x in line.split(":", 1))
+                info.setdefault(k, v)
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    ids = ", ".join(f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info)
+    return f"{info.get('model name', 'unknown')} ({ids})" if ids else info.get("model name", "unknown")
 
 
 def cpu_baseline(w):
     """Oracle fp32 host attention (restating tests/test_kernels.cu:94-108) over the full decode workload, on the
-    GPU's inputs, at 1 thread, 8 threads (the reference harness's cap, tests/test_flash_gemma.cu:342) and 16 threads
-    (this box's CPU share per GPU; the machine may list more CPUs). `value` is the 16-thread rate."""
+    GPU's inputs, at 1 thread, 8 threads (the reference harness's cap, tests/test_flash_gemma.cu:342) and every CPU
+    this process may run on (its affinity set). `value` is the all-CPU rate and `cores` that thread count."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     B, NQ, NKV, HD, ML = w["B"], w["NQ"], w["NKV"], w["HD"], w["ML"]
@@ -237,20 +245,22 @@ def cpu_baseline(w):
         affinity = len(os.sched_getaffinity(0))
     except AttributeError:
         affinity = os.cpu_count() or 1
+    sweep = sorted({1, min(8, affinity), affinity})
     rates = {}
-    for threads in (1, 8, 16):
+    for threads in sweep:
         t0 = time.perf_counter()
         oracle.attention(q, K, V, kv_off, lens - 1, NQ, NKV, HD, mode=1, nthreads=threads)
         dt = time.perf_counter() - t0
         rates[threads] = (nbytes / dt / 1e9, dt)
-    v16, dt16 = rates[16]
-    return dict(value=round(v16, 3), unit="GB/s", cores=16, kind="port",
-                threads_1_gbs=round(rates[1][0], 3), threads_8_gbs=round(rates[8][0], 3),
-                threads_16_gbs=round(v16, 3), host_cpus=os.cpu_count(), affinity_cpus=affinity,
-                cpu_model=_cpu_model(),
-                sample=f"full decode workload (16 rows x 24 heads, sum L = {int(lens.sum())} keys), fp32 host "
-                       f"attention (fp64 dot, fp32 softmax); ms per call at 1/8/16 threads: "
-                       f"{rates[1][1] * 1e3:.1f}/{rates[8][1] * 1e3:.1f}/{dt16 * 1e3:.1f}")
+    vall, dtall = rates[affinity]
+    out = dict(value=round(vall, 3), unit="GB/s", cores=affinity, kind="port")
+    out.update({f"threads_{t}_gbs": round(rates[t][0], 3) for t in sweep})
+    out.update(host_cpus=os.cpu_count(), affinity_cpus=affinity, cpu_model=_cpu_model(),
+               sample=f"full decode workload (16 rows x 24 heads, sum L = {int(lens.sum())} keys), fp32 host "
+                      f"attention (fp64 dot, fp32 softmax); ms per call at "
+                      f"{'/'.join(str(t) for t in sweep)} threads: "
+                      f"{'/'.join(f'{rates[t][1] * 1e3:.1f}' for t in sweep)}")
+    return out
 
 
 def run_global_decode(steps, warmup, seed=13):
@@ -364,7 +374,10 @@ def main():
         nms, nby = run_norm_rope(args.steps, args.warmup)
         extra["norm_rope_store_T1024"] = dict(us=round(nms * 1e3, 2), gbs=round(nby / (nms * 1e-3) / 1e9, 1))
         tms, tby = run_tree(args.steps, args.warmup)
-        extra["tree_verify_B16x8"] = dict(us=round(tms * 1e3, 2), gbs=round(tby / (tms * 1e-3) / 1e9, 1))
+        extra["tree_verify_B16x8"] = dict(us=round(tms * 1e3, 2), gbs=round(tby / (tms * 1e-3) / 1e9, 1),
+                                          runs="per-sequence chunks (batch-invariant)")
+        tms, tby = run_tree(args.steps, args.warmup, runs=1)
+        extra["tree_verify_B16x8_equal_runs"] = dict(us=round(tms * 1e3, 2), gbs=round(tby / (tms * 1e-3) / 1e9, 1))
         gms, gby, gkms = run_global_decode(args.steps, args.warmup)
         extra["decode_global_hd512_B8"] = dict(us=round(gms * 1e3, 2), gbs=round(gby / (gms * 1e-3) / 1e9, 1),
                                                kernel_us=round(gkms * 1e3, 2),

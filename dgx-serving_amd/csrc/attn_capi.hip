@@ -4,11 +4,14 @@
 #include "attn_internal.h"
 #include "../../include/dgx_attn.h"
 #include <climits>
+#include <atomic>
+#include <cerrno>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
+#include <map>
 #include <mutex>
 #include <string>
 
@@ -17,37 +20,99 @@ using namespace dgx;
 namespace {
 
 // ---------------------------------------------------------------- knobs
-// Resolution order of the reference registry (runtime/knobs.h:9-13, 297-303): env > DGX_KNOBS_FILE > unset.
-// Recipe lines are NAME=VALUE with '#' comments.
-const char *knob_raw(const char *name) {
-    if (const char *v = getenv(name)) return v;
-    static std::string path;
-    static std::string cache[8][2];
-    static int ncache = -1;
-    static std::mutex mu;
-    std::lock_guard<std::mutex> lock(mu);
-    if (ncache < 0) {
-        ncache = 0;
-        if (const char *p = getenv("DGX_KNOBS_FILE")) {
-            std::ifstream in(p);
-            std::string line;
-            while (in && std::getline(in, line) && ncache < 8) {
-                const size_t h = line.find('#'); if (h != std::string::npos) line.resize(h);
-                const size_t eq = line.find('='); if (eq == std::string::npos) continue;
-                auto trim = [](std::string t) { const size_t a = t.find_first_not_of(" \t\r"), b = t.find_last_not_of(" \t\r");
-                                                return a == std::string::npos ? std::string() : t.substr(a, b - a + 1); };
-                const std::string k = trim(line.substr(0, eq));
-                if (k.rfind("G4_ATTN", 0) == 0 || k.rfind("G4_KV", 0) == 0) { cache[ncache][0] = k; cache[ncache][1] = trim(line.substr(eq + 1)); ncache++; }
-            }
+// The attention subsystem's slice of the reference registry (runtime/knobs.h:49-69, 130-131): these names, their
+// value sets and the resolution order env > DGX_KNOBS_FILE recipe > default (runtime/knobs.h:9-13, 297-303). The
+// recipe format and checks follow runtime/knobs.h:241-275: '#' comments, NAME=VALUE lines, a line without '=' or
+// with an empty name is an error, a name under this subsystem's prefixes (G4_ATTN_, G4_KV_, G4_FLASH_) that is not
+// registered is an error, and every set value (env or recipe) must be in its set. Names under other prefixes
+// belong to other subsystems and are skipped. Where the reference exits with status 2, the C ABI reports the
+// first error once on stderr and the knob queries return -1 (dgx_knobs_status; the C++ wrapper exits 2).
+struct KnobDef { const char *name, *allowed; bool int_min1; };
+const KnobDef kKnobs[] = {
+    {"G4_ATTN_SPLIT", "0|1", false},          {"G4_ATTN_CHUNK", "32|64|128|256", false},
+    {"G4_KV_DTYPE", "fp32|f16|bf16", false},  {"G4_FLASH_PREFILL", "0|1", false},
+    {"G4_FLASH_MIN_S", "1..", true},          {"G4_FLASH_V2", "0|1", false},
+    {"G4_FLASH_F16_MMA", "0|1", false},       {"G4_KV_STATS", "0|1", false},
+    {"G4_ATTN_DIAG_REVERSE", "0|1", false},
+};
+const char *const kKnobPrefixes[] = {"G4_ATTN_", "G4_KV_", "G4_FLASH_"};
+
+const KnobDef *knob_find(const std::string &n) {
+    for (const KnobDef &k : kKnobs) if (n == k.name) return &k;
+    return nullptr;
+}
+bool knob_valid(const KnobDef &k, const char *v) {
+    if (k.int_min1) {
+        char *end = nullptr;
+        errno = 0;
+        const long x = strtol(v, &end, 10);
+        return errno == 0 && end != v && *end == '\0' && x >= 1;
+    }
+    const std::string set = std::string("|") + k.allowed + "|", item = std::string("|") + v + "|";
+    return *v && set.find(item) != std::string::npos;
+}
+
+struct KnobState {
+    bool ok = true;
+    std::string err;
+    std::map<std::string, std::string> recipe;
+};
+KnobState knob_load() {
+    KnobState s;
+    auto fail = [&](const std::string &m) { if (s.ok) { s.ok = false; s.err = m; } };
+    if (const char *path = getenv("DGX_KNOBS_FILE")) {
+        std::ifstream in(path);
+        if (!in) fail(std::string("cannot read DGX_KNOBS_FILE=") + path);
+        std::string line;
+        int n = 0;
+        auto trim = [](const std::string &t) {
+            const size_t a = t.find_first_not_of(" \t\r"), b = t.find_last_not_of(" \t\r");
+            return a == std::string::npos ? std::string() : t.substr(a, b - a + 1);
+        };
+        while (in && std::getline(in, line)) {
+            n++;
+            const size_t h = line.find('#');
+            if (h != std::string::npos) line.resize(h);
+            line = trim(line);
+            if (line.empty()) continue;
+            const size_t eq = line.find('=');
+            if (eq == std::string::npos || eq == 0) { fail(std::string(path) + ":" + std::to_string(n) + ": expected NAME=VALUE"); continue; }
+            const std::string key = trim(line.substr(0, eq)), val = trim(line.substr(eq + 1));
+            bool ours = false;
+            for (const char *pre : kKnobPrefixes) if (key.compare(0, strlen(pre), pre) == 0) ours = true;
+            if (ours && !knob_find(key)) { fail(std::string(path) + ": unknown knob " + key); continue; }
+            s.recipe[key] = val;
         }
     }
-    for (int i = 0; i < ncache; i++) if (cache[i][0] == name) return cache[i][1].c_str();
-    return nullptr;
+    for (const KnobDef &k : kKnobs) {
+        const char *v = getenv(k.name), *src = "env";
+        auto it = s.recipe.find(k.name);
+        if (!v && it != s.recipe.end()) { v = it->second.c_str(); src = "recipe"; }
+        if (v && !knob_valid(k, v))
+            fail(std::string("invalid ") + k.name + "=" + v + " (" + src + "); allowed: " + k.allowed);
+    }
+    if (!s.ok) fprintf(stderr, "knobs: %s\n", s.err.c_str());
+    return s;
+}
+const KnobState &knob_state() {
+    static const KnobState s = knob_load();
+    return s;
+}
+
+// Value of a registered knob as set by env or the recipe file, nullptr when unset or when the knob configuration
+// is invalid (callers then fail; see dgx_knobs_status).
+const char *knob_raw(const char *name) {
+    const KnobState &s = knob_state();
+    if (!s.ok) return nullptr;
+    if (const char *v = getenv(name)) return v;
+    auto it = s.recipe.find(name);
+    return it == s.recipe.end() ? nullptr : it->second.c_str();
 }
 
 int g_kv_override = -1;
 
 int parse_kv_dtype() {
+    if (!knob_state().ok) return -1;
     const char *v = knob_raw("G4_KV_DTYPE");
     if (!v || !*v) {
         const char *split = knob_raw("G4_ATTN_SPLIT");
@@ -61,6 +126,7 @@ int parse_kv_dtype() {
 }
 
 int parse_chunk() {
+    if (!knob_state().ok) return -1;
     int c = 256;                                  // MI355X default (the GB10 reference defaults to 64)
     if (const char *v = knob_raw("G4_ATTN_CHUNK")) {
         c = atoi(v);
@@ -180,13 +246,14 @@ struct Timing {
 };
 Timing g_timing;
 std::mutex g_timing_mu;
+std::atomic<bool> g_timing_on{false};
 
 template <class F>
 hipError_t timed_launch(hipStream_t st, F &&launch) {
     int slot = -1;
-    if (g_timing.on) {
+    if (g_timing_on.load(std::memory_order_acquire)) {            // atomic flag; the slots under the mutex
         std::lock_guard<std::mutex> lk(g_timing_mu);
-        if (g_timing.n < kTimed) slot = g_timing.n++;
+        if (g_timing.on && g_timing.n < kTimed) slot = g_timing.n++;
     }
     if (slot >= 0) { hipError_t e = hipEventRecord(g_timing.a[slot], st); if (e != hipSuccess) return e; }
     hipError_t e = launch();
@@ -194,9 +261,14 @@ hipError_t timed_launch(hipStream_t st, F &&launch) {
     return e;
 }
 
+// How verify_kernel cuts its runs (dgx_attn_verify_runs): 0 = each sequence's absolute key chunks, 1 = equal runs
+// over the whole batch.
+std::atomic<int> g_verify_runs{0};
+
 hipError_t run_split(const Problem &p, int chunk, Pool &pool, int ns_cap, hipStream_t st) {
     Partials part{pool.m, pool.l, pool.acc, ns_cap};
-    hipError_t e = timed_launch(st, [&] { return launch_split(p, chunk, part, st); });
+    const bool slot_runs = g_verify_runs.load(std::memory_order_relaxed) == 0;
+    hipError_t e = timed_launch(st, [&] { return launch_split(p, chunk, part, st, slot_runs); });
     if (e != hipSuccess) return e;
     return launch_combine(p, chunk, part, st);
 }
@@ -229,6 +301,13 @@ bool f32_take_fast(const Problem &p, const Pool *&pool) {
 }  // namespace
 
 extern "C" {
+
+int dgx_knobs_status(void) { return knob_state().ok ? 0 : -1; }
+
+int dgx_attn_verify_runs(int mode) {
+    if (mode == 0 || mode == 1) return g_verify_runs.exchange(mode);
+    return mode == -1 ? g_verify_runs.load() : -1;
+}
 
 size_t dgx_flash_attn_hd512_lds(void) {
     const size_t a = split_lds_bytes(512), b = prefill_lds_bytes(512);
@@ -556,6 +635,7 @@ hipError_t dgx_attn_timing(int on) {
     }
     g_timing.on = on != 0;
     g_timing.n = 0;
+    g_timing_on.store(on != 0, std::memory_order_release);
     return hipSuccess;
 }
 

@@ -66,8 +66,10 @@ __device__ __forceinline__ int win_lo(int pos, int window) {
     return (window > 0 && pos - window + 1 > 0) ? pos - window + 1 : 0;
 }
 
-// Split-KV decode / verify / tree kernel (waves split the keys of a chunk, small query-row tiles).
-hipError_t launch_split(const Problem &p, int chunk, Partials &part, hipStream_t st);
+// Split-KV decode / verify / tree kernel (waves split the keys of a chunk, small query-row tiles). Verify and tree
+// rows on 16-bit caches at HD <= 256 run verify_kernel: slot_runs cuts its runs at absolute key chunks of each
+// sequence (batch-invariant), otherwise into equal runs over the whole batch (faster, depends on the batch).
+hipError_t launch_split(const Problem &p, int chunk, Partials &part, hipStream_t st, bool slot_runs = true);
 // Streaming decode kernel (T x GRP <= 16 rows per KV head, HD 128/256, 16-bit cache);
 // hipErrorNotSupported for other shapes. Writes chunk partials for launch_combine.
 bool decode_stream_supported(const Problem &p);

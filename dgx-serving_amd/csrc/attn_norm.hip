@@ -14,7 +14,10 @@
 //     same lane (chunk index + hd/512); for power-of-two hd up to 256 it sits in lane l ^ (hd/8), one cross-lane
 //     swap; any other hd (a multiple of 4) takes its partners from the row staged in the wave's LDS slice. The
 //     products and the difference / sum are rounded separately: o = t1*c - t2*s, o' = t2*c + t1*s with cos/sin
-//     from the row p of the tables (entries [p*hd, p*hd + hd/2)).
+//     from the row p of the tables (entries [p*hd, p*hd + hd/2)). This is a deliberate choice, not a copy of the
+//     reference's rounding: the reference writes the same expressions (norm_fused.cuh:119-120) but its compiler
+//     may contract one product into an FMA, so its fp32 results can differ from these by about one ulp; the
+//     tests compare against the fp64 oracle.
 //   * Store: p = pos_arr ? pos_arr[s] : base + s * pos_step, row at Y + s*slot_stride + p*row_stride + h*hd, in
 //     fp32 or rounded to nearest-even f16 / bf16 (as kv_store_kernel converts).
 #include "attn_device.h"

@@ -25,8 +25,9 @@
 // Invariants (kept from the reference, attention_decode_split.cuh:8-12) for split_kernel: chunk and tile
 // boundaries are absolute key positions and the chunk combine runs in fixed order. A row's result therefore does
 // not depend on the batch, the other rows of its tile, the grid size or the maximum position: a row is
-// bit-identical alone or as a batch row. verify_kernel gives up the batch independence for the equal runs (its
-// run boundaries follow the total key count); its results are deterministic for given inputs.
+// bit-identical alone or as a batch row. verify_kernel keeps this in its default mode (slot_runs: partials at
+// absolute key chunks of each sequence); its other mode gives it up for equal runs (boundaries that follow the total
+// key count), deterministic for given inputs.
 #include "attn_device.h"
 #include "attn_internal.h"
 #include <algorithm>
@@ -42,6 +43,7 @@ struct SplitArgs {
     int tpb;        // query tokens per workgroup
     int nchunks;    // token tiles per sequence
     float sl2;      // scale * log2(e)
+    int slot_runs = 1;   // verify_kernel: 1 = runs are each pair's absolute key chunks (batch-invariant), 0 = equal runs
 };
 
 // Wave-wide reductions over all 64 lanes (fixed xor-butterfly order, identical result in every lane).
@@ -62,6 +64,11 @@ __device__ __forceinline__ float wave_sum(float v) {
 // writes one partial per pair it meets, into slot (run index - index of the pair's first run); the last run of a
 // pair marks the slot after its own for the combine. q depends on the total tile count, so verify results depend
 // on the batch; they are deterministic for given inputs.
+// With slot_runs (the default) each cut moves forward to the next absolute key-chunk boundary of its pair (C keys),
+// and a run flushes its state into partial slot (key / C) at every chunk boundary it crosses: the float operations
+// of a chunk then start from a fresh state at the chunk's first key whatever run holds it, so a row's result
+// depends only on its own sequence (the combine reads slots lo / C .. pos / C as for split_kernel). The cost is the
+// cut granularity: runs differ by up to C keys.
 struct SegPair { int seq, tok0, tok1, lo, hi, jb, n; };
 
 __device__ __forceinline__ SegPair seg_pair(const Problem &p, int tpb, int nchunks, int z) {
@@ -670,6 +677,20 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
     const unsigned kaddr = lds0 + ln * ROWB + ((g ^ kswz(ln)) << 4);
     const unsigned vaddr = lds0 + Cf::TILE + vr * ROWB + 8 * (ln & 1) + ((((ln & 3) >> 1) ^ vswz(vr)) << 4);
 
+    // The rows' partial (slot `sl`); `mark`: the slot after it ends the pair's slots for the combine.
+    const int r_out = seq * p.T + tq, h_out = kvh * GRP + rho % GRP;
+    auto write = [&](int sl, bool mark) {
+        const float ls = sum_over_groups(l);
+        if (!valid) return;
+        const size_t pi = ((size_t)r_out * p.NQ + h_out) * a.part.ns_cap + sl;
+#pragma unroll
+        for (int db = 0; db < DB; db++) *reinterpret_cast<f32x4 *>(a.part.acc + pi * HD + 16 * db + 4 * g) = acc[db];
+        if (g == 0) {
+            a.part.m[pi] = m; a.part.l[pi] = ls;
+            if (mark && sl + 1 < a.part.ns_cap) a.part.m[pi + 1] = kPosInf;
+        }
+    };
+
     for (int it = 0; it < ntile; it++) {
         // The barrier makes every wave's loads of tile it visible and frees the stage of tile it-1 for tile it+NS-1.
         wait_tile(it);
@@ -729,18 +750,17 @@ __device__ __forceinline__ void verify_segment(const SplitArgs &a, const SegPair
 #pragma unroll
             for (int j = 0; j < 8; j++) acc[d8 + j] = mfma_pv16<F16>(v[j], pop, acc[d8 + j]);
         }
+        if (a.slot_runs && it + 1 < ntile && (jt + KT) % a.C == 0) {
+            // The tile ends an absolute key chunk: its partial goes to slot (chunk index), the next chunk starts
+            // from a fresh state (the same float operations as a run that starts at that chunk).
+            write(jt / a.C, false);
+            m = kNegInf; l = 0.f;
+#pragma unroll
+            for (int db = 0; db < DB; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");        // no load may land after the workgroup ends
-    l = sum_over_groups(l);
-    if (!valid) return;
-    const int r = seq * p.T + tq, h = kvh * GRP + rho % GRP;
-    const size_t pi = ((size_t)r * p.NQ + h) * a.part.ns_cap + slot;
-#pragma unroll
-    for (int db = 0; db < DB; db++) *reinterpret_cast<f32x4 *>(a.part.acc + pi * HD + 16 * db + 4 * g) = acc[db];
-    if (g == 0) {
-        a.part.m[pi] = m; a.part.l[pi] = l;
-        if (last && slot + 1 < a.part.ns_cap) a.part.m[pi + 1] = kPosInf;   // end of the pair's slots
-    }
+    write(a.slot_runs ? (jb + KT * (ntile - 1)) / a.C : slot, last && !a.slot_runs);
 }
 
 template <int HD, int RB, int KVT, int QT>
@@ -775,21 +795,49 @@ __global__ void __launch_bounds__(256) verify_kernel(const SplitArgs a) {
     int N, z, P, pz;
     if (small) N = __builtin_amdgcn_readfirstlane(__shfl(incl, 63));
     else seg_scan(p, a.tpb, a.nchunks, INT_MAX, 0, N, z, P, pz);
-    const int q = max((N + G1 - 1) / G1, a.part.seg_qmin);
-    const long long xs = (long long)run * q;
-    if (xs >= N) return;
-    int x = (int)xs;
-    const int x1 = (int)min((long long)N, xs + q);
-    if (small) {
-        z = __builtin_amdgcn_readfirstlane(__builtin_ctzll(__ballot(incl > x)));
-        P = __builtin_amdgcn_readfirstlane(__shfl(incl, z) - __shfl(mine.n, z));
+    // Pair z holding tile x of the list, and the tiles before it (P).
+    auto locate = [&](int x) {
+        if (small) {
+            z = __builtin_amdgcn_readfirstlane(__builtin_ctzll(__ballot(incl > x)));
+            P = __builtin_amdgcn_readfirstlane(__shfl(incl, z) - __shfl(mine.n, z));
+        } else {
+            int n_;
+            seg_scan(p, a.tpb, a.nchunks, x, 0, n_, z, P, pz);
+        }
+    };
+    int x, x1;
+    if (a.slot_runs) {
+        // Equal runs, each end moved forward to the next absolute key-chunk boundary of its pair (or the pair's
+        // end): every chunk of a pair falls in one run, which writes it to partial slot (first key / C).
+        const int q = (N + G1 - 1) / G1, C = a.C;
+        auto snap = [&](long long xl) -> int {
+            if (xl >= N) return N;
+            const int xx = (int)xl;
+            locate(xx);
+            const int t = xx - P;
+            if (t == 0) return xx;
+            const SegPair s = pair_at(z);
+            const int kb = (s.jb + 16 * t + C - 1) / C * C;
+            return P + min((kb - s.jb) / 16, s.n);
+        };
+        x1 = snap((long long)(run + 1) * q);
+        x = snap((long long)run * q);
+        if (x >= x1) return;
+        locate(x);                                        // the snap may have moved x to the next pair
     } else {
-        seg_scan(p, a.tpb, a.nchunks, x, 0, N, z, P, pz);
+        const int q = max((N + G1 - 1) / G1, a.part.seg_qmin);
+        const long long xs = (long long)run * q;
+        if (xs >= N) return;
+        x = (int)xs;
+        x1 = (int)min((long long)N, xs + q);
+        locate(x);
     }
+    const int q = max((N + G1 - 1) / G1, a.part.seg_qmin);
     SegPair sp = pair_at(z);
     for (;;) {
-        const int t0 = x - P, t1 = min(sp.n, t0 + (x1 - x)), slot = run - P / q;
+        const int t0 = x - P, t1 = min(sp.n, t0 + (x1 - x)), slot = a.slot_runs ? 0 : run - P / q;
         if (slot < 0 || slot >= a.part.ns_cap) break;     // unreachable while the counts agree
+        if (t0 >= t1) break;                              // unreachable: x lies inside pair z
         verify_segment<HD, RB, KVT, QT>(a, sp, kvh, t0, t1, slot, t1 == sp.n, smem);
         x += t1 - t0;
         if (x >= x1) break;
@@ -842,8 +890,10 @@ static hipError_t launch_split_t(SplitArgs &a, dim3 grid, hipStream_t st) {
             // floor((n - 1) / q) + 2 runs (with fewer than ns_cap, the slot after the last holds the end mark).
             const int nmax = a.p.max_pos / 16 + 1;
             G = std::max(a.p.NKV, G - G % a.p.NKV);          // the same G / NKV runs for every KV head
-            a.part.seg_g = G;
-            a.part.seg_qmin = std::max(8, (nmax - 1) / (a.part.ns_cap - 1) + 1);
+            if (!a.slot_runs) {
+                a.part.seg_g = G;
+                a.part.seg_qmin = std::max(8, (nmax - 1) / (a.part.ns_cap - 1) + 1);
+            }
             hipLaunchKernelGGL((verify_kernel<HD, RB, KVT, QT>), dim3(G), dim3(256), VerifyCfg<HD>::LDS, st, a);
             return hipGetLastError();
         }
@@ -897,7 +947,7 @@ size_t partial_rows(const Problem &p, int chunk) {
     return (size_t)p.nseq * p.T * p.NQ * (size_t)(p.max_pos / chunk + 1);
 }
 
-hipError_t launch_split(const Problem &p, int chunk, Partials &part, hipStream_t st) {
+hipError_t launch_split(const Problem &p, int chunk, Partials &part, hipStream_t st, bool slot_runs) {
     part.seg_g = 0;
     if (chunk <= 0 || chunk % 16) return hipErrorInvalidValue;
     // Up to 16 rows per KV head (one query token at GRP <= 16): the streaming decode kernel.
@@ -909,7 +959,7 @@ hipError_t launch_split(const Problem &p, int chunk, Partials &part, hipStream_t
     split_tiling(p, RB, tpb, nchunks);
     if (RB * 16 < GRP || RB > 4) return hipErrorInvalidValue;
     if (p.max_pos / chunk + 1 > part.ns_cap) return hipErrorInvalidValue;
-    SplitArgs a{p, part, chunk, tpb, nchunks, p.scale * kLog2e};
+    SplitArgs a{p, part, chunk, tpb, nchunks, p.scale * kLog2e, slot_runs ? 1 : 0};
     dim3 grid(p.NKV, p.max_pos / chunk + 1, p.nseq * nchunks);
     if (grid.z > 65535u || grid.y > 65535u) return hipErrorInvalidConfiguration;
     if ((long long)p.nseq * p.NKV * (p.max_pos / 16 + 2) > INT_MAX) return hipErrorInvalidConfiguration;

@@ -26,6 +26,8 @@ def lib():
         L = ctypes.CDLL(LIB_PATH)
         P, I, F, L64, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_long, ctypes.c_size_t
         sig = {
+            "dgx_knobs_status": ([], I),
+            "dgx_attn_verify_runs": ([I], I),
             "dgx_kv_dtype": ([], I),
             "dgx_kv_force_fp32": ([ctypes.c_char_p], None),
             "dgx_kv_elem": ([], S),
@@ -87,6 +89,20 @@ def kv_code(t):
 
 
 # ------------------------------------------------------------------ drop-in entry points
+def knobs_status():
+    """0 when the attention knobs (env and DGX_KNOBS_FILE) are valid, -1 otherwise (dgx_knobs_status)."""
+    return lib().dgx_knobs_status()
+
+
+def verify_runs(mode=-1):
+    """Set how the batched verify kernel divides the keys (0: each sequence's absolute chunks, batch-invariant, the
+    default; 1: equal runs over the batch); -1 queries. Returns the previous mode (dgx_attn_verify_runs)."""
+    r = lib().dgx_attn_verify_runs(mode)
+    if r < 0 and mode != -1:
+        raise ValueError(f"verify_runs: mode {mode} is not 0, 1 or -1")
+    return r
+
+
 def split_chunk():
     return lib().dgx_attn_split_chunk()
 

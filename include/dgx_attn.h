@@ -33,8 +33,25 @@ extern "C" {
 
 /* ---- knobs (runtime/knobs.h registry semantics: env > DGX_KNOBS_FILE recipe > default) ---- */
 
+/* 0 when the attention knobs are valid, -1 otherwise (the first error is printed once, "knobs: ..."): a recipe line
+ * that is not NAME=VALUE, an unregistered name under G4_ATTN_ / G4_KV_ / G4_FLASH_, an unreadable DGX_KNOBS_FILE,
+ * or a value outside its set (G4_ATTN_SPLIT, G4_ATTN_CHUNK, G4_KV_DTYPE, G4_FLASH_PREFILL, G4_FLASH_MIN_S,
+ * G4_FLASH_V2, G4_FLASH_F16_MMA, G4_KV_STATS, G4_ATTN_DIAG_REVERSE). With an invalid configuration the knob queries
+ * below return -1. Replaces the registry load and its exit(2), runtime/knobs.h:241-275 (the C++ wrapper exits 2). */
+int dgx_knobs_status(void);
+
+/* How the batched verify / tree kernel (16-bit caches, HD <= 256, more than one query token) divides the keys
+ * among its workgroups, process-wide. mode 0 (the default): each sequence's keys in absolute chunks of the split
+ * chunk, so a row's result depends only on its own sequence, bit-identical to the same slot launched alone (the
+ * reference verifies each slot with its own launch, models/qwen35_batch.cu:333-335). mode 1: equal runs over the
+ * whole batch's key tiles (every workgroup streams the same bytes; results are deterministic but depend on the other
+ * sequences' lengths). mode -1 queries. Returns the previous mode, or -1 for another value. No reference
+ * counterpart: the reference has only the per-slot behaviour of mode 0. */
+int dgx_attn_verify_runs(int mode);
+
 /* Process-wide KV storage dtype from G4_KV_DTYPE (fp32 | f16 | bf16; unset -> f16, or fp32 when
- * G4_ATTN_SPLIT=0). Returns -1 for an invalid value (the C++ wrapper exits 1 like the reference).
+ * G4_ATTN_SPLIT=0). Returns -1 for an invalid value or knob configuration (the C++ wrapper exits 2 like the
+ * reference registry).
  * Replaces g4_kv_dtype(), kernels/kv_store.cuh:23-35. */
 int dgx_kv_dtype(void);
 /* Dynamic LDS bytes of the head-dim 512 flash path (the larger of its short-query split and prefill tiles; each
@@ -50,7 +67,7 @@ void dgx_kv_force_fp32(const char *why);
 size_t dgx_kv_elem(void);
 
 /* Split-KV chunk from G4_ATTN_CHUNK (32, 64, 128 or 256, the reference's set; unset -> 256 on MI355X, where the
- * reference defaults to 64). -1 if invalid.
+ * reference defaults to 64). -1 if invalid (value or knob configuration).
  * Replaces attn_split_chunk(), kernels/attention_decode_split.cuh:26-37. */
 int dgx_attn_split_chunk(void);
 /* ceil(max_len / chunk). Replaces attn_split_ns_cap(), kernels/attention_decode_split.cuh:173. */
@@ -80,7 +97,10 @@ hipError_t dgx_attn_decode_split(const float *Q, const void *Kc, const void *Vc,
 hipError_t dgx_flash_attn(const float *Q, const void *Kc, const void *Vc, int kv_dtype, float *O, float *lse,
                           int Sq, int NQ, int NKV, int HD, int base, hipStream_t st, const unsigned *anc,
                           float scale, int window);
-/* Pre-size the flash scratch for Sq tokens at base. Replaces reserve_flash_attn_scratch(), attention_flash.cuh:236. */
+/* Pre-size the flash scratch for Sq tokens at base (runs of up to 32 tokens; longer runs without a tree mask take
+ * the prefill kernel and need none). A tree-masked run of more than 32 tokens needs
+ * dgx_flash_attn_reserve_partials(Sq * NQ * ((base + Sq - 1) / 512 + 1), HD) before graph capture.
+ * Replaces reserve_flash_attn_scratch(), attention_flash.cuh:236. */
 hipError_t dgx_flash_attn_reserve(int Sq, int NQ, int base, int HD);
 /* Pre-size the flash scratch to `partials` (row, head, split) partials of hd_max floats, the reference's own
  * unit. Replaces reserve_flash_attn_scratch(need, hd), attention_flash.cuh:236-252. */

@@ -4,7 +4,7 @@
 // kernels/attention.cuh, attention_decode_split.cuh, attention_flash.cuh, attention_flash_v2.cuh and
 // kv_store.cuh and compile unchanged apart from the CUDA -> HIP type names (cudaStream_t -> hipStream_t,
 // __nv_bfloat16 -> __hip_bfloat16). Every wrapper keeps the reference's name, argument order, defaults and error
-// convention (fprintf to stderr, then abort(); an invalid knob exits 1). All kernels live in libdgx_attn.so.
+// convention (fprintf to stderr, then abort(); an invalid knob exits 2, runtime/knobs.h:240). All kernels live in libdgx_attn.so.
 #ifndef DGX_ATTN_HPP
 #define DGX_ATTN_HPP
 #include <cstddef>
@@ -34,16 +34,24 @@ template <class KV> constexpr int kv_code() {
 }
 }  // namespace dgx_detail
 
+// runtime/knobs.h:240-275: an invalid knob configuration (recipe syntax, unknown name, value out of its set) ends
+// the process with status 2 at the first knob read.
+inline void g4_knobs_check() {
+    if (dgx_knobs_status() < 0) exit(2);
+}
+
 // ---- kernels/kv_store.cuh:25-113
 inline int g4_kv_dtype() {
+    g4_knobs_check();
     const int d = dgx_kv_dtype();
-    if (d < 0) exit(1);                         // the reference exits on an invalid G4_KV_DTYPE (kv_store.cuh:36)
+    if (d < 0) exit(2);
     return d;
 }
 inline void g4_kv_force_fp32(const char *why) { dgx_kv_force_fp32(why); }
 // kernels/kv_store.cuh:87-99: G4_KV_STATS=1 turns the store statistics on; they are reported once at exit.
 static inline bool g4_kv_stats_enabled() {
     static const bool on = []() {
+        g4_knobs_check();
         if (!dgx_kv_stats_enabled()) return false;
         atexit([]() {
             unsigned h[4] = {0, 0, 0, 0};
@@ -124,8 +132,9 @@ static inline void launch_attn_decode_batch(const float *Q, const float *Kc, con
 
 // ---- kernels/attention_decode_split.cuh:26-231 (cache dtype from g4_kv_dtype(), float* handles)
 static inline int attn_split_chunk() {
+    g4_knobs_check();
     const int c = dgx_attn_split_chunk();
-    if (c < 0) exit(1);
+    if (c < 0) exit(2);
     return c;
 }
 static inline int attn_split_ns_cap(int max_len) { const int C = attn_split_chunk(); return (max_len + C - 1) / C; }

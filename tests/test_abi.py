@@ -46,7 +46,7 @@ def _knobs(env):
         import ctypes
         L = ctypes.CDLL({LIB!r})
         print(L.dgx_kv_dtype(), L.dgx_attn_split_chunk(), L.dgx_attn_split_ns_cap(1000), L.dgx_kv_elem(),
-              L.dgx_kv_stats_enabled())
+              L.dgx_kv_stats_enabled(), L.dgx_knobs_status())
     """)
     e = {k: v for k, v in os.environ.items() if not k.startswith(("G4_", "DGX_KNOBS"))}
     e.update(env)
@@ -56,22 +56,50 @@ def _knobs(env):
 
 
 def test_kv_dtype_and_chunk_knobs(tmp_path):
-    assert _knobs({})[0] == [1, 256, 4, 2, 0]                      # unset -> f16; MI355X chunk default 256
+    assert _knobs({})[0] == [1, 256, 4, 2, 0, 0]                   # unset -> f16; MI355X chunk default 256
     assert _knobs({"G4_KV_STATS": "1"})[0][4] == 1                  # g4_kv_stats_enabled (kv_store.cuh:87-90)
     assert _knobs({"G4_ATTN_SPLIT": "0"})[0][0] == 0                # split off -> fp32 KV (kv_store.cuh:29-31)
     assert _knobs({"G4_KV_DTYPE": "bf16"})[0][0] == 2
     assert _knobs({"G4_KV_DTYPE": "fp32"})[0][:4] == [0, 256, 4, 4]
     v, err = _knobs({"G4_KV_DTYPE": "fp8"})
-    assert v[0] == -1 and "Invalid G4_KV_DTYPE" in err
+    assert v[0] == -1 and v[5] == -1 and "invalid G4_KV_DTYPE=fp8 (env)" in err
     assert _knobs({"G4_ATTN_CHUNK": "64"})[0][1:3] == [64, 16]
     for bad in ("100", "512"):                                      # the reference's set is 32/64/128/256
         v, err = _knobs({"G4_ATTN_CHUNK": bad})
-        assert v[1] == -1 and "Invalid G4_ATTN_CHUNK" in err
+        assert v[1] == -1 and "invalid G4_ATTN_CHUNK" in err
     recipe = tmp_path / "recipe.env"
     recipe.write_text("# recipe\nG4_KV_DTYPE = bf16  # comment\nG4_ATTN_CHUNK=128\n")
     assert _knobs({"DGX_KNOBS_FILE": str(recipe)})[0][:2] == [2, 128]
     # env beats the recipe (runtime/knobs.h precedence)
     assert _knobs({"DGX_KNOBS_FILE": str(recipe), "G4_KV_DTYPE": "f16"})[0][:2] == [1, 128]
+
+
+@pytest.mark.parametrize("text,msg", [
+    ("G4_KV_DTYPE=bf16\nnot a knob line\n", "recipe.env:2: expected NAME=VALUE"),
+    ("=bf16\n", "recipe.env:1: expected NAME=VALUE"),
+    ("G4_ATTN_CHUNKS=64\n", "unknown knob G4_ATTN_CHUNKS"),
+    ("G4_FLASH_F16_MMA=2\n", "invalid G4_FLASH_F16_MMA=2 (recipe)"),
+    ("G4_FLASH_MIN_S=0\n", "invalid G4_FLASH_MIN_S=0 (recipe)"),
+    ("G4_ATTN_SPLIT=yes\n", "invalid G4_ATTN_SPLIT=yes (recipe)"),
+])
+def test_recipe_errors_fail_like_the_registry(tmp_path, text, msg):
+    """runtime/knobs.h:241-275: malformed lines, unregistered names under the subsystem's prefixes and values out
+    of their set make every knob query fail (the reference exits 2)."""
+    recipe = tmp_path / "recipe.env"
+    recipe.write_text(text)
+    v, err = _knobs({"DGX_KNOBS_FILE": str(recipe)})
+    assert v[0] == -1 and v[1] == -1 and v[5] == -1, v
+    assert f"knobs: " in err and msg in err, err
+
+
+def test_recipe_skips_other_subsystems_and_reads_every_attention_knob(tmp_path):
+    recipe = tmp_path / "recipe.env"
+    recipe.write_text("MMQ_TILE=4  # another subsystem's knob\nG4_MMQ_PREFILL=1\nG4_FLASH_MIN_S=17\n"
+                      "G4_FLASH_V2=0\nG4_KV_STATS=1\n\n   # blank and comment lines\n")
+    v, err = _knobs({"DGX_KNOBS_FILE": str(recipe)})
+    assert v == [1, 256, 4, 2, 1, 0], (v, err)
+    v, err = _knobs({"DGX_KNOBS_FILE": str(tmp_path / "missing.env")})
+    assert v[5] == -1 and "cannot read DGX_KNOBS_FILE" in err
 
 
 def test_force_fp32_overrides():
@@ -156,3 +184,6 @@ def test_reference_style_caller_compiles_and_links(tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60, env=e)
     assert out.returncode == 0, out.stderr
     assert out.stdout.split() == ["1", "256", "32", "2", "20"]
+    # an invalid knob ends a reference-style caller with status 2 (runtime/knobs.h:240)
+    bad = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60, env=dict(e, G4_ATTN_CHUNK="100"))
+    assert bad.returncode == 2 and "invalid G4_ATTN_CHUNK=100" in bad.stderr, (bad.returncode, bad.stderr)

@@ -71,6 +71,31 @@ def test_tree_verify_graph_replays_with_new_bases():
         assert torch.equal(Og.view(torch.int16), Oe.view(torch.int16)), f"replay {step} bases {b.tolist()}"
 
 
+def test_long_tree_flash_graph_after_reserve_partials():
+    """A tree-masked flash run of 40 tokens (more than 32) goes to the split kernel; with its partials reserved
+    through dgx_flash_attn_reserve_partials the captured call allocates nothing and replays like the eager one."""
+    Sq, NQ, NKV, HD, base = 40, 16, 4, 256, 700
+    L = base + Sq
+    K, V = _cache(9, 1, L, NKV, HD)[0], _cache(10, 1, L, NKV, HD)[0]
+    Q = torch.randn(Sq * NQ * HD, device="cuda")
+    anc = np.array([(1 << (min(t, 31) + 1)) - 1 if t % 3 else (1 << min(t, 31)) | 1 for t in range(Sq)],
+                   np.uint64).astype(np.uint32)
+    ancd = torch.from_numpy(anc.view(np.int32)).cuda()
+    A.flash_reserve_partials(Sq * NQ * ((base + Sq - 1) // 512 + 1), HD)
+    Og = torch.empty(Sq * NQ * HD, device="cuda"); Oe = torch.empty_like(Og)
+    A.flash_attn(Q, K, V, Og, Sq, NQ, NKV, HD, base, anc=ancd)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        A.flash_attn(Q, K, V, Og, Sq, NQ, NKV, HD, base, anc=ancd)
+    for step in range(3):
+        Q.copy_(torch.randn(Sq * NQ * HD, device="cuda"))
+        g.replay()
+        A.flash_attn(Q, K, V, Oe, Sq, NQ, NKV, HD, base, anc=ancd)
+        torch.cuda.synchronize()
+        assert torch.equal(Og.view(torch.int32), Oe.view(torch.int32)), f"replay {step}"
+
+
 def test_prefill_graph_replays_with_new_queries():
     T, NQ, NKV, HD = 256, 16, 8, 256
     g0 = torch.Generator(device="cuda").manual_seed(5)

@@ -110,3 +110,56 @@ def test_ragged_tree_verify_shapes(kvdt, HD, NQ, NKV, Tq):
                                tree_base=np.repeat(base_b, Tq))
     assert_close(O.cpu().numpy().reshape(B * Tq, NQ, HD), ref, f"tree HD{HD} Tq{Tq} kv{kvdt}",
                  lse.cpu().numpy().reshape(-1, NQ), ref_lse)
+
+
+def _run_batch(q, kd, vd, B, Tq, NQ, NKV, HD, ML, base_b, anc, chunk):
+    max_pos = int((base_b + Tq - 1).max())
+    O = torch.empty(B * Tq * NQ * HD, device="cuda"); lse = torch.empty(B * Tq * NQ, device="cuda")
+    A.attn_batch(q, kd, vd, O, B, Tq, NQ, NKV, HD, dev(base_b), ML * NKV * HD, max_pos, chunk=chunk,
+                 anc=None if anc is None else dev(anc.reshape(-1).view(np.int32)), lse=lse)
+    torch.cuda.synchronize()
+    return O.cpu().numpy().reshape(B, Tq, NQ, HD), lse.cpu().numpy().reshape(B, Tq, NQ)
+
+
+@pytest.mark.parametrize("chunk", [0, 512])
+@pytest.mark.parametrize("shape", ["config5", "hd128_tiles", "verify_chain"])
+def test_slot_alone_equals_slot_in_batch(shape, chunk):
+    """A slot's verify rows are bit-identical whether it is launched alone or as one slot of a batch (the reference
+    launches every slot on its own, models/qwen35_batch.cu:333-335): B = 16 trees of 8 nodes at config 5's heads,
+    HD 128 with several token tiles per sequence, and a plain causal chain of 8 draft tokens."""
+    assert A.verify_runs(-1) == 0, "the batch-invariant run mode is the default"
+    if shape == "config5":
+        B, NQ, NKV, HD, Tq, lo, hi = 16, 24, 4, 256, 8, 2048, 16384
+    elif shape == "hd128_tiles":
+        B, NQ, NKV, HD, Tq, lo, hi = 16, 16, 4, 128, 20, 1, 5000
+    else:
+        B, NQ, NKV, HD, Tq, lo, hi = 16, 16, 2, 256, 8, 300, 9000
+    committed = oracle.gen_uniform_int(91 + HD + Tq, lo, hi, B).astype(np.int32)
+    anc = None
+    if shape != "verify_chain":
+        parents = [oracle.tree_random(700 + b, Tq, 2, 7)[0] for b in range(B)]
+        anc = np.stack([oracle.tree_anc(p) for p in parents]).astype(np.uint32)
+    ML = hi + Tq
+    lens = committed + Tq
+    _, kd = normal_cache(92, B, ML, NKV, HD, lens, 0.5, 1)
+    _, vd = normal_cache(93, B, ML, NKV, HD, lens, 0.5, 1)
+    q = dev(oracle.gen_normal(94, B * Tq * NQ * HD))
+    A.split_reserve(B * Tq, NQ, int(lens.max()), HD)
+    Ob, Lb = _run_batch(q, kd, vd, B, Tq, NQ, NKV, HD, ML, committed, anc, chunk)
+    row = ML * NKV * HD
+    kf, vf = kd.reshape(-1), vd.reshape(-1)
+    for b in range(B):
+        qs = q[b * Tq * NQ * HD:(b + 1) * Tq * NQ * HD]
+        Os, Ls = _run_batch(qs, kf[b * row:(b + 1) * row], vf[b * row:(b + 1) * row], 1, Tq, NQ, NKV, HD, ML,
+                            committed[b:b + 1], None if anc is None else anc[b:b + 1], chunk)
+        assert np.array_equal(Os[0].view(np.uint32), Ob[b].view(np.uint32)), f"{shape} chunk {chunk}: slot {b} O"
+        assert np.array_equal(Ls[0].view(np.uint32), Lb[b].view(np.uint32)), f"{shape} chunk {chunk}: slot {b} lse"
+
+
+def test_equal_runs_mode_against_oracle():
+    """The other run mode (equal runs over the batch's key tiles) on config 5's tree verify, against the oracle."""
+    prev = A.verify_runs(1)
+    try:
+        test_config5_batched_tree_verify("random8")
+    finally:
+        A.verify_runs(prev)
