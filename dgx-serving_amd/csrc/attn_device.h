@@ -173,6 +173,17 @@ __device__ __forceinline__ f32x4 mfma_pv32(const u32x4 &v, const PFrag<F16> &p0,
     if constexpr (!F16) c = mfma16<F16>(v, u32x4{p0.lo[0], p0.lo[1], p1.lo[0], p1.lo[1]}, c);
     return c;
 }
+// The hi and lo halves of mfma_pv32 on their own (the same two products in the same order), so that a batch of
+// independent accumulators can issue all hi products before the lo products that depend on them.
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma_pv32_hi(const u32x4 &v, const PFrag<F16> &p0, const PFrag<F16> &p1, f32x4 c) {
+    return mfma16<F16>(v, u32x4{p0.hi[0], p0.hi[1], p1.hi[0], p1.hi[1]}, c);
+}
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma_pv32_lo(const u32x4 &v, const PFrag<F16> &p0, const PFrag<F16> &p1, f32x4 c) {
+    if constexpr (!F16) c = mfma16<F16>(v, u32x4{p0.lo[0], p0.lo[1], p1.lo[0], p1.lo[1]}, c);
+    return c;
+}
 
 // LDS transpose read (gfx950 ds_read_b64_tr_b16). Within each 16-lane group g, lane i passes the address of
 // row 4g + i/4, columns 4*(i%4)..+3 of a row-major 16-bit tile; lane n of the group receives column n of

@@ -428,8 +428,12 @@ prefill_kernel(const PrefArgs a) {
                 }
 #pragma unroll
                 for (int j = 0; j < PB; j++)
-                    acc[0][b * PB + j] = mfma_pv32<F16>(u32x4{cur[2 * j][0], cur[2 * j][1], cur[2 * j + 1][0], cur[2 * j + 1][1]},
-                                                        pop[0][0], pop[1][0], acc[0][b * PB + j]);
+                    acc[0][b * PB + j] = mfma_pv32_hi<F16>(u32x4{cur[2 * j][0], cur[2 * j][1], cur[2 * j + 1][0], cur[2 * j + 1][1]},
+                                                           pop[0][0], pop[1][0], acc[0][b * PB + j]);
+#pragma unroll
+                for (int j = 0; j < PB; j++)
+                    acc[0][b * PB + j] = mfma_pv32_lo<F16>(u32x4{cur[2 * j][0], cur[2 * j][1], cur[2 * j + 1][0], cur[2 * j + 1][1]},
+                                                           pop[0][0], pop[1][0], acc[0][b * PB + j]);
                 if (pt < NPART && b % 2 == 1) issue_pt(nxt, pt++);
             }
         }
