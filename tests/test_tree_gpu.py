@@ -163,3 +163,41 @@ def test_equal_runs_mode_against_oracle():
         test_config5_batched_tree_verify("random8")
     finally:
         A.verify_runs(prev)
+
+
+@pytest.mark.parametrize("runs", [0, 1])
+def test_verify_more_than_64_pairs(runs):
+    """72 sequences x 12 tokens (one token tile each: 72 (sequence, tile) pairs, past the 64 that the kernel keeps in
+    lanes, so the run cuts come from scans over the positions), ragged lengths from 1 key, half of them trees, HD 128
+    bf16, both run modes against the oracle; in the default mode three slots alone equal their rows in the batch."""
+    B, NQ, NKV, HD, Tq = 72, 8, 4, 128, 12
+    committed = oracle.gen_uniform_int(501, 0, 700, B).astype(np.int32)
+    anc = np.stack([oracle.tree_anc(oracle.tree_random(900 + b, Tq, 3, 6)[0]) if b % 2 else
+                    oracle.tree_anc(np.arange(-1, Tq - 1)) for b in range(B)]).astype(np.uint32)
+    ML = 700 + Tq
+    lens = committed + Tq
+    kv, kd = normal_cache(502, B, ML, NKV, HD, lens, 0.5, 2)
+    vv, vd = normal_cache(503, B, ML, NKV, HD, lens, 0.5, 2)
+    q = oracle.gen_normal(504, B * Tq * NQ * HD)
+    qr, _ = oracle.round_to(q, 2)
+    A.split_reserve(B * Tq, NQ, int(lens.max()), HD)
+    prev = A.verify_runs(runs)
+    try:
+        Ob, Lb = _run_batch(dev(qr), kd, vd, B, Tq, NQ, NKV, HD, ML, committed, anc, 256)
+        if runs == 0:
+            row = ML * NKV * HD
+            kf, vf = kd.reshape(-1), vd.reshape(-1)
+            qd = dev(qr)
+            for b in (0, 35, 71):
+                Os, Ls = _run_batch(qd[b * Tq * NQ * HD:(b + 1) * Tq * NQ * HD], kf[b * row:(b + 1) * row],
+                                    vf[b * row:(b + 1) * row], 1, Tq, NQ, NKV, HD, ML, committed[b:b + 1],
+                                    anc[b:b + 1], 256)
+                assert np.array_equal(Os[0].view(np.uint32), Ob[b].view(np.uint32)), f"slot {b} O"
+                assert np.array_equal(Ls[0].view(np.uint32), Lb[b].view(np.uint32)), f"slot {b} lse"
+    finally:
+        A.verify_runs(prev)
+    pos = (committed[:, None] + np.arange(Tq)[None, :]).reshape(-1)
+    kv_off = np.repeat(np.arange(B, dtype=np.int64) * ML * NKV * HD, Tq)
+    ref, ref_lse = oracle_rows(qr, kv, vv, kv_off, pos, NQ, NKV, HD, anc=anc.reshape(-1),
+                               tree_base=np.repeat(committed, Tq))
+    assert_close(Ob.reshape(B * Tq, NQ, HD), ref, f"72 pairs runs {runs}", Lb.reshape(-1, NQ), ref_lse)
