@@ -159,12 +159,15 @@ __device__ __forceinline__ f32x4 mfma16k16(const u32x2 &a, const u32x2 &b, const
 }
 
 
-// acc += V^T P^T with the P fragment split as above (hi, then lo for bf16).
-template <bool F16>
+// acc += V^T P^T over 16 keys with the P fragment split as above. f16: one 16x16x16 MFMA. bf16: hi and lo share one
+// 16x16x32 MFMA, whose reduction runs over (the lane's 4 keys with hi, the same 4 keys with lo) against the V
+// fragment given twice: on gfx950 a 16x16x32 issues in the time of a 16x16x16, so the lo products cost nothing.
+// PACK = false keeps two 16x16x16 MFMAs (fewer live operand registers, for kernels at the register limit).
+template <bool F16, bool PACK = true>
 __device__ __forceinline__ f32x4 mfma_pv16(const u32x2 &v, const PFrag<F16> &p, f32x4 c) {
-    c = mfma16k16<F16>(v, p.hi, c);
-    if constexpr (!F16) c = mfma16k16<F16>(v, p.lo, c);
-    return c;
+    if constexpr (F16) return mfma16k16<F16>(v, p.hi, c);
+    else if constexpr (PACK) return mfma16<F16>(u32x4{v[0], v[1], v[0], v[1]}, u32x4{p.hi[0], p.hi[1], p.lo[0], p.lo[1]}, c);
+    else return mfma16k16<F16>(v, p.lo, mfma16k16<F16>(v, p.hi, c));
 }
 // The 16x16x32 form over two sub-tiles: B = (P of sub-tile 0, P of sub-tile 1) in k-groups of 4 keys.
 template <bool F16>

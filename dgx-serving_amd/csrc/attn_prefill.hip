@@ -438,8 +438,8 @@ prefill_kernel(const PrefArgs a) {
             }
         }
         if constexpr (NSUB != 2) {
-            // Software-pipelined PV: batch b = 8 dim blocks of one sub-tile; batch b+1 is read before batch b's MFMAs.
-            constexpr int PB = 8, NPB = NSUB * DB / PB;
+            // Software-pipelined PV: batch b = 4 dim blocks of one sub-tile; batch b+1 is read before batch b's MFMAs.
+            constexpr int PB = 4, NPB = NSUB * DB / PB;
             u32x2 vb2[2][PB];
             auto rdv = [&](int b, u32x2 (&dst)[PB]) {
                 const int sub = b / (DB / PB), d0 = (b % (DB / PB)) * PB;
@@ -453,16 +453,14 @@ prefill_kernel(const PrefArgs a) {
                 u32x2 (&cur)[PB] = vb2[b & 1];
                 if (b + 1 < NPB) {
                     rdv(b + 1, vb2[(b + 1) & 1]);
-                    asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]),
-                                 "+v"(cur[5]), "+v"(cur[6]), "+v"(cur[7])::"memory");
+                    asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3])::"memory");
                 } else {
-                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3]), "+v"(cur[4]),
-                                 "+v"(cur[5]), "+v"(cur[6]), "+v"(cur[7])::"memory");
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(cur[0]), "+v"(cur[1]), "+v"(cur[2]), "+v"(cur[3])::"memory");
                 }
                 const int sub = b / (DB / PB), d0 = (b % (DB / PB)) * PB;
 #pragma unroll
-                for (int j = 0; j < PB; j++) acc[0][d0 + j] = mfma_pv16<F16>(cur[j], pop[sub][0], acc[0][d0 + j]);
-                if (pt < NPART && b % 2 == 1) issue_pt(nxt, pt++);
+                for (int j = 0; j < PB; j++) acc[0][d0 + j] = mfma_pv16<F16, KVT != DT_FP32>(cur[j], pop[sub][0], acc[0][d0 + j]);
+                if (pt < NPART && b % 4 == 3) issue_pt(nxt, pt++);
             }
         }
         while (pt < NPART) issue_pt(nxt, pt++);
