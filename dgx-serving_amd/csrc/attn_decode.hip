@@ -52,7 +52,8 @@ struct DecodeCfg {
 // Work item blockIdx.x -> (sequence, chunk c, kv head blockIdx.x % NKV), enumerating only the chunks that hold keys
 // of the sequence's tokens (kv head fastest): the workgroups with work come first in launch order and the dispatcher
 // spreads them over all CUs; the tail of the upper-bound grid (false) exits at once. Two phases: first every chunk
-// of each sequence but its last, then the last chunks (the partial ones). The dispatcher hands workgroups out in
+// of each sequence but one, then that one: the shorter of its first and last chunk (both partial under a sliding
+// window, only the last otherwise). The dispatcher hands workgroups out in
 // index order and a CU that receives more workgroups than the others shares its bandwidth among them, so the short
 // items go last, where they land on the CUs that get a third workgroup (measured: a CU with three full items runs
 // 20% longer than one with two).
@@ -72,6 +73,13 @@ __device__ __forceinline__ bool find_item(const Problem &p, int C, int &seq, int
                 n = max(0, min((hi_s - 1) / C, cmax) - first + 1);
             }
             const int m = phase == 0 ? max(n - 1, 0) : min(n, 1);   // items of this sequence in this phase
+            // The phase-1 chunk: the shorter of the first and the last chunk (a sliding window's first chunk is
+            // partial too); phase 0 takes the others in order.
+            int sh = 0;
+            if (n >= 2) {
+                const int kf = min(hi_s, (first + 1) * C) - lo_s, kl = hi_s - max(lo_s, (first + n - 1) * C);
+                sh = kf < kl ? 0 : n - 1;
+            }
             int incl = m;                                  // inclusive prefix sum over the 64 lanes
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
@@ -82,8 +90,12 @@ __device__ __forceinline__ bool find_item(const Problem &p, int C, int &seq, int
             if (hit) {
                 const int l = __builtin_ctzll(hit);
                 seq = s0 + l;
-                c = phase == 0 ? __shfl(first, l) + rest - (__shfl(incl, l) - __shfl(m, l))
-                               : __shfl(first, l) + __shfl(n, l) - 1;
+                if (phase == 0) {
+                    const int r = rest - (__shfl(incl, l) - __shfl(m, l));
+                    c = __shfl(first, l) + (r < __shfl(sh, l) ? r : r + 1);
+                } else {
+                    c = __shfl(first, l) + __shfl(sh, l);
+                }
                 lo = __shfl(lo_s, l); hi = __shfl(hi_s, l);
                 return true;
             }
