@@ -150,9 +150,9 @@ def run_sliding_decode(steps, warmup, seed=9):
     Q = torch.randn(B * NQ * HD, device="cuda", generator=g).bfloat16()
     O = torch.empty_like(Q)
     pos = torch.from_numpy(lens - 1).cuda()
-    chunk = int(os.environ.get("BENCH_SLIDING_CHUNK", "128"))
+    chunk = int(os.environ.get("BENCH_SLIDING_CHUNK", "96"))
     A.split_reserve(B * max(1, -(-A.split_chunk() // chunk)), NQ, ML, HD)   # partials for the chunk
-    # a 1K window spans few 256-key chunks: 128-key chunks give twice the workgroups (20.8 vs 23.7 us measured)
+    # a 1K window spans few 256-key chunks: 96-key chunks measured fastest (18.6 us; 128: 19.5, 160: 19.7, 256: 24)
     fn = lambda: A.attn_batch(Q, K, V, O, B, 1, NQ, NKV, HD, pos, ML * NKV * HD, int(lens.max()) - 1, chunk=chunk,
                               window=W)
     ms = timed(fn, steps, warmup)

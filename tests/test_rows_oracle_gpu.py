@@ -3,7 +3,7 @@ full workload.
 
 - Config 4b (sliding-window batched decode, the Gemma local layer as models/gemma4_batch.cu:173-174 calls it):
   B=8, context lengths U[1024, 32768] seeded, window 1024, Hq=16 Hkv=8 hd=256, bf16 KV and bf16 Q/O, through
-  dgx_attn_batch at chunk 128 (the benchmark's) and at the library default, every row's O and LSE against the
+  dgx_attn_batch at chunk 96 (the benchmark's), 128 and the library default, every row's O and LSE against the
   fp64 oracle. Keys outside each row's window hold K = 0 and V = 64: a kernel that attended any of them would
   move the output by far more than the tolerance.
 - Per-slot K/V pointer tables (dgx_attn_batch_ex Kp/Vp; the per-slot caches of models/qwen35_batch.cu:165-167,
@@ -41,7 +41,7 @@ def _windows(seed, lens, NKV, HD, W, dt_code):
     return vals, bits
 
 
-@pytest.mark.parametrize("chunk", [128, 0])
+@pytest.mark.parametrize("chunk", [96, 128, 0])
 def test_config4b_sliding_decode_full_workload(chunk):
     B, NQ, NKV, HD, W, ML = 8, 16, 8, 256, 1024, 32768
     lens = oracle.gen_uniform_int(4242, 1024, ML, B)
