@@ -276,8 +276,9 @@ def run_global_decode(steps, warmup, seed=13):
     Q = torch.randn(B * NQ * HD, device="cuda", generator=g).bfloat16()
     O = torch.empty_like(Q)
     pos = torch.from_numpy(lens - 1).cuda()
-    A.split_reserve(B, NQ, ML, HD)
-    fn = lambda: A.attn_batch(Q, K, V, O, B, 1, NQ, NKV, HD, pos, ML * NKV * HD, int(lens.max()) - 1, chunk=512)
+    chunk = int(os.environ.get("BENCH_GLOBAL_CHUNK", "512"))    # 512 measured fastest (128-384: 93-103 us per call)
+    A.split_reserve(B * max(1, -(-A.split_chunk() // chunk)), NQ, ML, HD)
+    fn = lambda: A.attn_batch(Q, K, V, O, B, 1, NQ, NKV, HD, pos, ML * NKV * HD, int(lens.max()) - 1, chunk=chunk)
     ms, kms = timed(fn, steps, warmup, kernel=True)
     return ms, int(lens.sum()) * NKV * HD * 2 * 2 + 2 * Q.numel() * 2, kms
 
