@@ -10,10 +10,13 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <unistd.h>
 #include <fstream>
 #include <map>
 #include <mutex>
 #include <string>
+#include <vector>
+#include <algorithm>
 
 using namespace dgx;
 
@@ -24,8 +27,9 @@ namespace {
 // value sets and the resolution order env > DGX_KNOBS_FILE recipe > default (runtime/knobs.h:9-13, 297-303). The
 // recipe format and checks follow runtime/knobs.h:241-275: '#' comments, NAME=VALUE lines, a line without '=' or
 // with an empty name is an error, a name under this subsystem's prefixes (G4_ATTN_, G4_KV_, G4_FLASH_) that is not
-// registered is an error, and every set value (env or recipe) must be in its set. Names under other prefixes
-// belong to other subsystems and are skipped. Where the reference exits with status 2, the C ABI reports the
+// registered is an error, and every set value (env or recipe) must be in its set; an unregistered environment
+// name under those prefixes only warns (runtime/knobs.h:273-283). Names under other prefixes belong to other
+// subsystems and are skipped. Where the reference exits with status 2, the C ABI reports the
 // first error once on stderr and the knob queries return -1 (dgx_knobs_status; the C++ wrapper exits 2).
 struct KnobDef { const char *name, *allowed; bool int_min1; };
 const KnobDef kKnobs[] = {
@@ -50,6 +54,19 @@ bool knob_valid(const KnobDef &k, const char *v) {
     }
     const std::string set = std::string("|") + k.allowed + "|", item = std::string("|") + v + "|";
     return *v && set.find(item) != std::string::npos;
+}
+
+// Levenshtein distance (insert, delete, substitute: cost 1 each), two rolling rows.
+size_t edit_distance(const std::string &a, const std::string &b) {
+    std::vector<size_t> prev(b.size() + 1), cur(b.size() + 1);
+    for (size_t j = 0; j <= b.size(); j++) prev[j] = j;
+    for (size_t i = 1; i <= a.size(); i++) {
+        cur[0] = i;
+        for (size_t j = 1; j <= b.size(); j++)
+            cur[j] = std::min({prev[j] + 1, cur[j - 1] + 1, prev[j - 1] + (a[i - 1] == b[j - 1] ? 0 : 1)});
+        std::swap(prev, cur);
+    }
+    return prev[b.size()];
 }
 
 struct KnobState {
@@ -83,6 +100,24 @@ KnobState knob_load() {
             if (ours && !knob_find(key)) { fail(std::string(path) + ": unknown knob " + key); continue; }
             s.recipe[key] = val;
         }
+    }
+    // Environment names under this subsystem's prefixes that are not registered only warn (a likely typo: the
+    // closest registered name within 3 edits is suggested), as in the reference.
+    for (char **e = environ; e && *e; e++) {
+        const char *eqp = strchr(*e, '=');
+        if (!eqp) continue;
+        const std::string name(*e, eqp - *e);
+        bool ours = false;
+        for (const char *pre : kKnobPrefixes) if (name.compare(0, strlen(pre), pre) == 0) ours = true;
+        if (!ours || knob_find(name)) continue;
+        const KnobDef *best = nullptr;
+        size_t bd = 4;
+        for (const KnobDef &k : kKnobs) {
+            const size_t d = edit_distance(name, k.name);
+            if (d < bd) { bd = d; best = &k; }
+        }
+        if (best) fprintf(stderr, "knobs: warning: unknown knob env %s (did you mean %s?)\n", name.c_str(), best->name);
+        else fprintf(stderr, "knobs: warning: unknown knob env %s\n", name.c_str());
     }
     for (const KnobDef &k : kKnobs) {
         const char *v = getenv(k.name), *src = "env";

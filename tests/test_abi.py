@@ -102,6 +102,17 @@ def test_recipe_skips_other_subsystems_and_reads_every_attention_knob(tmp_path):
     assert v[5] == -1 and "cannot read DGX_KNOBS_FILE" in err
 
 
+def test_unknown_env_knob_under_our_prefix_warns():
+    """An environment name under the attention prefixes that is not registered only warns (runtime/knobs.h:273-283),
+    with the closest registered name when it is within 3 edits; the configuration stays valid."""
+    v, err = _knobs({"G4_ATTN_CHUNKS": "64"})
+    assert v[5] == 0 and "unknown knob env G4_ATTN_CHUNKS (did you mean G4_ATTN_CHUNK?)" in err, err
+    v, err = _knobs({"G4_KV_SOMETHING_ELSE": "1"})
+    assert v[5] == 0 and "unknown knob env G4_KV_SOMETHING_ELSE" in err and "did you mean" not in err, err
+    v, err = _knobs({"G4_MMQ_TILE": "4"})                     # another subsystem's prefix: silent
+    assert v[5] == 0 and "warning" not in err, err
+
+
 def test_force_fp32_overrides():
     code = textwrap.dedent(f"""
         import ctypes
