@@ -129,7 +129,9 @@ def run_tree(steps, warmup, seed=5, runs=None):
     ancd = torch.from_numpy(anc.reshape(-1).view(np.int32)).cuda()
     max_pos = int(committed.max()) + Tq - 1
     A.split_reserve(B * Tq, NQ, max_pos + 1, HD)
-    chunk = int(os.environ.get("BENCH_TREE_CHUNK", "512"))
+    # split chunk: a free parameter for tree verify (config 5 names none); with per-sequence chunk cuts 640 keys
+    # measured fastest (256: 166, 384: 149, 512: 147-150, 640: 140, 768: 144, 1024: 154 us per call)
+    chunk = int(os.environ.get("BENCH_TREE_CHUNK", "640"))
     # 0: per-sequence chunks (the library default, batch-invariant), 1: equal runs over the batch
     prev = A.verify_runs(int(os.environ.get("BENCH_VERIFY_RUNS", "0")) if runs is None else runs)
     fn = lambda: A.attn_batch(Q, K, V, O, B, Tq, NQ, NKV, HD, base_b, ML * NKV * HD, max_pos, chunk=chunk, anc=ancd)

@@ -121,7 +121,7 @@ def _run_batch(q, kd, vd, B, Tq, NQ, NKV, HD, ML, base_b, anc, chunk):
     return O.cpu().numpy().reshape(B, Tq, NQ, HD), lse.cpu().numpy().reshape(B, Tq, NQ)
 
 
-@pytest.mark.parametrize("chunk", [0, 512])
+@pytest.mark.parametrize("chunk", [0, 512, 640])
 @pytest.mark.parametrize("shape", ["config5", "hd128_tiles", "verify_chain"])
 def test_slot_alone_equals_slot_in_batch(shape, chunk):
     """A slot's verify rows are bit-identical whether it is launched alone or as one slot of a batch (the reference
